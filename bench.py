@@ -1,0 +1,258 @@
+"""Benchmark of the hot path on one MI355X.
+
+Workloads (synthetic seeded inputs, random-init weights of the named shapes):
+  * ResNet-50 v1.5, FP32 NCHW, batch 32: one step = one inference of the
+    batch through BuildEngine/ExecutionContext (53 fused conv nodes, MaxPool,
+    GAP, Flatten view, Gemm), replayed as one hipGraph. `value` is img/s.
+  * FP16 FFN block M=4096, H=1024, I=4096 (GemmGelu -> Gemm -> SkipLayerNorm):
+    reported as TFLOP/s of its two GEMMs beside the main line.
+
+Timing: W untimed warm-up steps, then K steps bracketed by
+torch.cuda.synchronize(); each step is RunAsync on the measured stream +
+Synchronize, as in the reference harness (benchmarks/resnet50_native.cpp:281-291).
+Per-op HIP event pairs recorded inside the graph (the engine's profiler)
+give each kernel's duration over the same timed steps; the dominant kernel
+family (the FP32 implicit-GEMM convolutions) is priced against the FP32
+MFMA peak from those durations.
+
+The CPU baseline is the reference's CPU path (the same graph in PyTorch-CPU
+FP32, oracle/torch_cpu.py) on a bounded sample, timed on this host.
+
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ResNet-50 fp32 img/s @bs32 (% FP32 MFMA peak); FFN fp16 TFLOP/s @M=4096"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2516.6
+CONV_OPS = ("FusedConvBatchNormRelu", "FusedConvBatchNorm", "FusedConvBatchNormAddRelu", "Conv")
+
+
+def log(*args) -> None:
+    print(*args, file=sys.stderr, flush=True)
+
+
+def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiling: bool):
+    """Builds and tunes `graph`, then times `steps` steps. Returns
+    (ms per step list, per-op total ms over the timed steps, plan ops)."""
+    import numpy as np
+    import torch
+
+    from cutriton_amd import engine, workloads
+
+    opts = engine.CompileOptions(tuning_mode="tune_on_miss", tuning_cache_dir=cache_dir,
+                                 enable_profiling=profiling, enable_hip_graph=True,
+                                 tuning_warmup_iterations=3, tuning_measurement_iterations=10)
+    eng = engine.build_engine(workloads.to_model(graph), opts)
+    ctx = eng.create_execution_context()
+    inputs = {n: torch.from_numpy(np.ascontiguousarray(v)).to("cuda:0") for n, v in feeds.items()}
+    for name, t in inputs.items():
+        ctx.bind_input(name, t, layout=graph.inputs[name][2])
+    outputs = {}
+    for name in graph.outputs:
+        shape, dtype = eng.value_desc(name)
+        outputs[name] = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
+        ctx.bind_output(name, outputs[name], layout="NCHW" if len(shape) == 4 else "")
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+    t0 = time.perf_counter()
+    ctx.run_async(handle)  # first run: tuning, module loads, graph capture
+    ctx.synchronize()
+    log(f"  first run (tuning + capture) {time.perf_counter() - t0:.1f} s")
+    for _ in range(warmup):
+        ctx.run_async(handle)
+        ctx.synchronize()
+    ops = eng.ops()
+    op_ms = [0.0] * len(ops)
+    step_ms = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for _ in range(steps):
+        start.record(stream)
+        ctx.run_async(handle)
+        end.record(stream)
+        ctx.synchronize()
+        step_ms.append(start.elapsed_time(end))
+        if profiling:
+            for i, (_, ms) in enumerate(ctx.profile_events()):
+                op_ms[i] += ms
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3
+    selected = [op.candidates[s] for op, s in zip(ops, ctx.selected_candidates(len(ops)))]
+    return step_ms, wall_ms, op_ms, ops, selected
+
+
+def bench_resnet(args, cache_dir: str) -> dict:
+    from cutriton_amd import workloads
+
+    batch = 32
+    graph = workloads.resnet50(batch)
+    x = workloads.resnet50_input(batch)
+    step_ms, wall_ms, op_ms, ops, selected = run_workload(graph, {"input": x}, args.steps, args.warmup,
+                                                         cache_dir, profiling=True)
+    flops = workloads.node_flops(graph)
+    conv_flops = sum(v for k, v in flops.items() if k != "classifier")
+    total_flops = sum(flops.values())
+    ms_per_step = wall_ms / args.steps
+    img_s = batch * 1e3 / ms_per_step
+    conv_idx = [i for i, op in enumerate(ops) if op.op_type in CONV_OPS]
+    conv_ms = sum(op_ms[i] for i in conv_idx) / args.steps
+    launches = len(conv_idx)
+    achieved = conv_flops / (conv_ms * 1e-3) / 1e12
+    per_op = sorted(((op_ms[i] / args.steps, ops[i].node_name, selected[i].split(":")[-1]) for i in range(len(ops))),
+                    reverse=True)
+    log(f"  resnet50 bs32: {ms_per_step:.3f} ms/step (event median {sorted(step_ms)[len(step_ms) // 2]:.3f}), "
+        f"{img_s:.1f} img/s, conv kernels {conv_ms:.3f} ms/step")
+    for ms, name, var in per_op[:12]:
+        log(f"    {ms * 1e3:8.1f} us  {name}  [{var}]")
+    return {
+        "ms_per_step": ms_per_step,
+        "img_s": img_s,
+        "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
+        "pct_fp32_mfma_peak": 100.0 * total_flops / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "roofline": {
+            "kernel": "conv_bn[_add]_relu_fp32 implicit-GEMM family (53 launches/step)",
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "flop_per_launch": conv_flops / launches,
+            "avg_launch_us": conv_ms * 1e3 / launches,
+        },
+        "selected": selected,
+    }
+
+
+def bench_ffn(args, cache_dir: str) -> dict:
+    from cutriton_amd import workloads
+
+    m, h, i = 4096, 1024, 4096
+    graph, x = workloads.ffn(m, h, i)
+    step_ms, wall_ms, op_ms, ops, selected = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir,
+                                                         profiling=True)
+    gemm_flops = 2 * m * h * i
+    per_op = {op.op_type: op_ms[j] / args.steps for j, op in enumerate(ops)}
+    ms_per_step = wall_ms / args.steps
+    out = {
+        "workload": f"ffn_fp16_m{m}_h{h}_i{i}",
+        "ms_per_step": ms_per_step,
+        "tflops_block": 2 * gemm_flops / (ms_per_step * 1e-3) / 1e12,
+        "gemm_gelu_us": per_op["GemmGelu"] * 1e3,
+        "gemm_us": per_op["Gemm"] * 1e3,
+        "skip_layer_norm_us": per_op["SkipLayerNormalization"] * 1e3,
+        "gemm_gelu_tflops": gemm_flops / (per_op["GemmGelu"] * 1e-3) / 1e12,
+        "gemm_tflops": gemm_flops / (per_op["Gemm"] * 1e-3) / 1e12,
+        "skip_layer_norm_gbps": 3 * m * h * 2 / (per_op["SkipLayerNormalization"] * 1e-3) / 1e9,
+        "selected": selected,
+    }
+    out["pct_fp16_mfma_peak_gemms"] = 100.0 * (2 * gemm_flops) / ((per_op["GemmGelu"] + per_op["Gemm"]) * 1e-3) \
+        / 1e12 / FP16_MFMA_PEAK_TFLOPS
+    log(f"  ffn: {ms_per_step * 1e3:.1f} us/step; GemmGelu {out['gemm_gelu_us']:.1f} us "
+        f"({out['gemm_gelu_tflops']:.0f} TF), Gemm {out['gemm_us']:.1f} us ({out['gemm_tflops']:.0f} TF), "
+        f"SkipLN {out['skip_layer_norm_us']:.1f} us")
+    return out
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The same ResNet-50 bs32 graph in PyTorch-CPU FP32, timed for about
+    `budget_s` seconds after one warm-up batch."""
+    import torch
+
+    from cutriton_amd import workloads
+    from oracle import torch_cpu
+
+    cores = os.cpu_count() or 1
+    # The host share of one GPU is capped by OMP_NUM_THREADS where it is set.
+    torch.set_num_threads(min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    batch = 32
+    graph = workloads.resnet50(batch)
+    consts = torch_cpu.prepare(graph)
+    x = torch.from_numpy(workloads.resnet50_input(batch))
+    torch_cpu.run(graph, consts, {"input": x})
+    times = []
+    t_start = time.perf_counter()
+    while not times or (time.perf_counter() - t_start < budget_s and len(times) < 10):
+        t0 = time.perf_counter()
+        torch_cpu.run(graph, consts, {"input": x})
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    cpu_model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(batch / med, 2),
+        "unit": "img/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"ResNet-50 bs32 FP32 PyTorch-CPU restatement of the same graph, {len(times)} batches after 1 "
+                  f"warm-up, median {med:.2f} s/batch; host {cpu_model} ({cores} logical CPUs)",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=30)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=("all", "resnet50", "ffn"), default="all")
+    parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
+                        help="bounded CPU sample; 0 skips the CPU baseline")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (cuda:0)", file=sys.stderr)
+        return 2
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    cache_dir = tempfile.mkdtemp(prefix="cutriton-tuning-")
+    result = {
+        "metric": METRIC, "value": None, "unit": "img/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic (seeded N(0,1) inputs, random-init weights)",
+        "config": {"workload": "resnet50_v1.5_fp32_nchw_bs32", "global_batch": 32, "image": [3, 224, 224],
+                   "parallelism": "single-gpu"},
+    }
+    if args.workload in ("all", "resnet50"):
+        r = bench_resnet(args, cache_dir)
+        result.update(value=round(r["img_s"], 2), ms_per_step=round(r["ms_per_step"], 4),
+                      pct_fp32_mfma_peak=round(r["pct_fp32_mfma_peak"], 2), roofline=r["roofline"])
+        result["resnet50_tflops"] = round(r["tflops"], 3)
+    if args.workload in ("all", "ffn"):
+        f = bench_ffn(args, cache_dir)
+        f.pop("selected", None)
+        result["ffn"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in f.items()}
+        if args.workload == "ffn":
+            result.update(value=round(f["tflops_block"], 3), unit="TFLOP/s", ms_per_step=round(f["ms_per_step"], 4),
+                          dtype="fp16", config={"workload": f["workload"], "parallelism": "single-gpu"})
+    if args.cpu_baseline_seconds > 0 and args.workload in ("all", "resnet50"):
+        result["cpu_baseline"] = cpu_baseline(args.cpu_baseline_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

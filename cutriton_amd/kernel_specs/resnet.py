@@ -1,0 +1,220 @@
+"""Pack entries of the FP32 CNN kernels (conv_fp32.hip, pool_fp32.hip,
+elementwise.hip).
+
+Argument order and sources are those of the reference pack
+(``python/cutriton/triton_kernels/resnet.py:216-400``), so a node binds the
+same values in the same order; the grids and variants are this backend's.
+``FusedConvBatchNormAddRelu`` and the 3-input FP32 Gemm have no reference
+kernel: they take the reference convolution / Gemm ABI with one more input.
+"""
+
+from __future__ import annotations
+
+from cutriton_amd.kernel_sdk.spec import (
+    KernelSpec,
+    KernelVariant,
+    arg,
+    ceil_div,
+    literal,
+    meta,
+    mul,
+    numel_grid,
+    output_dim,
+    register,
+    reserved,
+)
+
+CONV_SOURCE = "conv_fp32.hip"
+
+# (variant id, BLOCK_M, BLOCK_N, BLOCK_K); BLOCK_M tiles output channels and
+# BLOCK_N tiles (image, output pixel) columns.
+CONV_TILES = (
+    ("m128n128", 128, 128, 16),
+    ("m64n128", 64, 128, 32),
+    ("m128n64", 128, 64, 16),
+    ("m64n64", 64, 64, 32),
+)
+CONV_DEFAULT = "m128n128"
+
+CONV_DIMENSIONS = (
+    arg("n", "i32", "input_dim", index=0, axis=0),
+    arg("c", "i32", "input_dim", index=0, axis=1),
+    arg("h", "i32", "input_dim", index=0, axis=2),
+    arg("w", "i32", "input_dim", index=0, axis=3),
+    arg("k", "i32", "input_dim", index=1, axis=0),
+    arg("r", "i32", "input_dim", index=1, axis=2),
+    arg("s", "i32", "input_dim", index=1, axis=3),
+    arg("out_h", "i32", "output_dim", index=0, axis=2),
+    arg("out_w", "i32", "output_dim", index=0, axis=3),
+    arg("stride_h", "i32", "attribute_i64", name="strides", index=0, default=1),
+    arg("stride_w", "i32", "attribute_i64", name="strides", index=1, default=1),
+    arg("pad_h", "i32", "attribute_i64", name="pads", index=0, default=0),
+    arg("pad_w", "i32", "attribute_i64", name="pads", index=1, default=0),
+    arg("dilation_h", "i32", "attribute_i64", name="dilations", index=0, default=1),
+    arg("dilation_w", "i32", "attribute_i64", name="dilations", index=1, default=1),
+)
+
+# x: ceil(N*P*Q / BLOCK_N), y: ceil(K_out / BLOCK_M).
+CONV_GRID = (
+    ceil_div(mul(mul(output_dim(0), output_dim(2)), output_dim(3)), meta("BLOCK_N")),
+    ceil_div(output_dim(1), meta("BLOCK_M")),
+)
+
+
+def conv_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return tuple(
+        KernelVariant(
+            name,
+            f"{prefix}_{name}",
+            num_warps=4,
+            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk},
+            default=name == CONV_DEFAULT,
+        )
+        for name, bm, bn, bk in CONV_TILES
+    )
+
+
+def register_conv_family() -> None:
+    bn_inputs = tuple(
+        arg(name, "*fp32", "input", index=i)
+        for i, name in enumerate(("x", "weight", "scale", "bias", "mean", "variance"))
+    )
+    epsilon = arg("epsilon", "fp32", "attribute_f64", name="batchnorm_epsilon", default=1e-5)
+    for op_type, kernel_id, prefix, inputs in (
+        ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw.mfma", "conv_bn_relu_fp32", bn_inputs),
+        ("FusedConvBatchNorm", "conv_bn.fp32.nchw.mfma", "conv_bn_fp32", bn_inputs),
+        (
+            "FusedConvBatchNormAddRelu",
+            "conv_bn_add_relu.fp32.nchw.mfma",
+            "conv_bn_add_relu_fp32",
+            bn_inputs + (arg("residual", "*fp32", "input", index=6),),
+        ),
+    ):
+        arguments = inputs + (arg("output", "*fp32", "output", index=0),) + CONV_DIMENSIONS + (epsilon,) + reserved()
+        register(KernelSpec(
+            kernel_id, op_type, 1, CONV_SOURCE, arguments, CONV_GRID, conv_variants(prefix),
+            layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},),
+        ))
+    conv_arguments = (
+        arg("x", "*fp32", "input", index=0),
+        arg("weight", "*fp32", "input", index=1),
+        arg("output", "*fp32", "output", index=0),
+    ) + CONV_DIMENSIONS + reserved()
+    register(KernelSpec(
+        "conv.fp32.nchw.mfma", "Conv", 1, CONV_SOURCE, conv_arguments, CONV_GRID, conv_variants("conv_fp32"),
+        layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},),
+    ))
+
+
+def register_gemm() -> None:
+    # C[M,N] = A[M,K] B[K,N]: x = ceil(N / BLOCK_N), y = ceil(M / BLOCK_M).
+    grid = (ceil_div(output_dim(1), meta("BLOCK_N")), ceil_div(output_dim(0), meta("BLOCK_M")))
+    tiles = (("m64n64", 64, 64, 32), ("m128n128", 128, 128, 16))
+    dims = (
+        arg("m", "i32", "input_dim", index=0, axis=0),
+        arg("n", "i32", "input_dim", index=1, axis=1),
+        arg("k", "i32", "input_dim", index=0, axis=1),
+    )
+    common = (
+        {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
+        {"kind": "attribute_i64_eq", "name": "transB", "value": 0, "default": 0},
+        {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+        {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
+    )
+    for kernel_id, prefix, inputs, extra in (
+        ("gemm.fp32.mfma", "gemm_fp32", ("a", "b"), ()),
+        ("gemm_bias.fp32.mfma", "gemm_bias_fp32", ("a", "b", "bias"),
+         ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)),
+    ):
+        arguments = tuple(arg(name, "*fp32", "input", index=i) for i, name in enumerate(inputs)) + (
+            arg("output", "*fp32", "output", index=0),
+        ) + dims + reserved()
+        variants = tuple(
+            KernelVariant(name, f"{prefix}_{name}", num_warps=4,
+                          meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk}, default=name == "m64n64")
+            for name, bm, bn, bk in tiles
+        )
+        register(KernelSpec(
+            kernel_id, "Gemm", 1, CONV_SOURCE, arguments, grid, variants,
+            constraints=({"kind": "input_count_eq", "value": len(inputs)},) + common + extra,
+        ))
+
+
+def register_bandwidth_kernels() -> None:
+    def variants(symbol: str) -> tuple[KernelVariant, ...]:
+        return (KernelVariant("w4", symbol, num_warps=4, default=True),)
+
+    # Elementwise: 4 elements per thread, 256 threads per workgroup.
+    for kernel_id, op_type, symbol, inputs in (
+        ("relu.fp32.contiguous", "Relu", "relu_fp32", ("x",)),
+        ("add.fp32.contiguous", "Add", "add_fp32", ("a", "b")),
+        ("add_relu.fp32.contiguous", "AddRelu", "add_relu_fp32", ("a", "b")),
+    ):
+        arguments = tuple(arg(name, "*fp32", "input", index=i) for i, name in enumerate(inputs)) + (
+            arg("output", "*fp32", "output", index=0),
+            arg("total", "i32", "output_numel", index=0),
+        ) + reserved()
+        register(KernelSpec(
+            kernel_id, op_type, 1, "elementwise.hip", arguments, numel_grid(1024), variants(symbol),
+            constraints=({"kind": "input_count_eq", "value": len(inputs)},),
+        ))
+
+    bn_arguments = (
+        arg("x", "*fp32", "input", index=0),
+        arg("scale", "*fp32", "input", index=1),
+        arg("bias", "*fp32", "input", index=2),
+        arg("mean", "*fp32", "input", index=3),
+        arg("variance", "*fp32", "input", index=4),
+        arg("output", "*fp32", "output", index=0),
+        arg("total", "i32", "output_numel", index=0),
+        arg("channels", "i32", "input_dim", index=0, axis=1),
+        arg("spatial", "i32", "input_dim_product", index=0, begin_axis=2),
+        arg("epsilon", "fp32", "attribute_f64", name="epsilon", alternate_name="batchnorm_epsilon", default=1e-5),
+    ) + reserved()
+    register(KernelSpec(
+        "batch_norm.fp32.nchw", "BatchNormalization", 1, "elementwise.hip", bn_arguments, numel_grid(1024),
+        variants("batch_norm_fp32_nchw"), layout="NCHW",
+    ))
+
+    pool_arguments = (
+        arg("x", "*fp32", "input", index=0),
+        arg("output", "*fp32", "output", index=0),
+        arg("n", "i32", "input_dim", index=0, axis=0),
+        arg("c", "i32", "input_dim", index=0, axis=1),
+        arg("h", "i32", "input_dim", index=0, axis=2),
+        arg("w", "i32", "input_dim", index=0, axis=3),
+        arg("out_h", "i32", "output_dim", index=0, axis=2),
+        arg("out_w", "i32", "output_dim", index=0, axis=3),
+        arg("kernel_h", "i32", "attribute_i64", name="kernel_shape", index=0, default=1),
+        arg("kernel_w", "i32", "attribute_i64", name="kernel_shape", index=1, default=1),
+        arg("stride_h", "i32", "attribute_i64", name="strides", index=0, default=1),
+        arg("stride_w", "i32", "attribute_i64", name="strides", index=1, default=1),
+        arg("pad_h", "i32", "attribute_i64", name="pads", index=0, default=0),
+        arg("pad_w", "i32", "attribute_i64", name="pads", index=1, default=0),
+        arg("dilation_h", "i32", "attribute_i64", name="dilations", index=0, default=1),
+        arg("dilation_w", "i32", "attribute_i64", name="dilations", index=1, default=1),
+    ) + reserved()
+    register(KernelSpec(
+        "max_pool.fp32.nchw", "MaxPool", 1, "pool_fp32.hip", pool_arguments, numel_grid(256),
+        variants("max_pool_fp32_nchw"), layout="NCHW",
+    ))
+
+    gap_arguments = (
+        arg("x", "*fp32", "input", index=0),
+        arg("output", "*fp32", "output", index=0),
+        arg("n", "i32", "input_dim", index=0, axis=0),
+        arg("c", "i32", "input_dim", index=0, axis=1),
+        arg("h", "i32", "input_dim", index=0, axis=2),
+        arg("w", "i32", "input_dim", index=0, axis=3),
+    ) + reserved()
+    # One 64-plane wavefront per 64 (image, channel) pairs, 4 per workgroup.
+    register(KernelSpec(
+        "global_average_pool.fp32.nchw", "GlobalAveragePool", 1, "pool_fp32.hip", gap_arguments,
+        (ceil_div(mul(output_dim(0), output_dim(1)), literal(256)),),
+        variants("global_average_pool_fp32_nchw"), layout="NCHW",
+    ))
+
+
+register_conv_family()
+register_gemm()
+register_bandwidth_kernels()

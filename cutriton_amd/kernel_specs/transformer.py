@@ -1,0 +1,129 @@
+"""Pack entries of the FP16 FFN kernels (gemm_fp16.hip, layer_norm_fp16.hip,
+elementwise.hip).
+
+Argument order and sources follow the reference pack
+(``python/cutriton/triton_kernels/transformer.py:193-371``): Gemm/GemmGelu
+take ``a, b, output, m, n, k`` with m and n read from the output. The
+3-input (bias) Gemm/GemmGelu entries are additions of this backend: they
+insert ``bias`` (input 2) after ``b``.
+"""
+
+from __future__ import annotations
+
+from cutriton_amd.kernel_sdk.spec import (
+    KernelSpec,
+    KernelVariant,
+    arg,
+    ceil_div,
+    literal,
+    meta,
+    mul,
+    numel_grid,
+    output_dim,
+    register,
+    reserved,
+)
+
+GEMM_SOURCE = "gemm_fp16.hip"
+
+# (variant id, BLOCK_M, BLOCK_N, BLOCK_K, wavefronts)
+GEMM_TILES = (
+    ("m64n64k64", 64, 64, 64, 2),
+    ("m128n128k64", 128, 128, 64, 4),
+    ("m256n128k64", 256, 128, 64, 4),
+    ("m256n256k64", 256, 256, 64, 8),
+)
+GEMM_DEFAULT = "m128n128k64"
+
+# One workgroup per output tile: ceil(M / BLOCK_M) * ceil(N / BLOCK_N).
+GEMM_GRID = (mul(ceil_div(output_dim(0), meta("BLOCK_M")), ceil_div(output_dim(1), meta("BLOCK_N"))),)
+
+GEMM_DIMS = (
+    arg("m", "i32", "output_dim", index=0, axis=0),
+    arg("n", "i32", "output_dim", index=0, axis=1),
+    arg("k", "i32", "input_dim", index=0, axis=1),
+)
+
+GEMM_CONSTRAINTS = (
+    {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
+    {"kind": "attribute_i64_eq", "name": "transB", "value": 0, "default": 0},
+    {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+    {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
+)
+
+
+def gemm_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return tuple(
+        KernelVariant(
+            name, f"{prefix}_{name}", num_warps=waves,
+            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk}, default=name == GEMM_DEFAULT,
+        )
+        for name, bm, bn, bk, waves in GEMM_TILES
+    )
+
+
+def register_gemms() -> None:
+    for kernel_id, op_type, prefix, bias in (
+        ("gemm.fp16.mfma", "Gemm", "gemm_fp16", False),
+        ("gemm_gelu.fp16.mfma", "GemmGelu", "gemm_gelu_fp16", False),
+        ("gemm_bias.fp16.mfma", "Gemm", "gemm_bias_fp16", True),
+        ("gemm_gelu_bias.fp16.mfma", "GemmGelu", "gemm_gelu_bias_fp16", True),
+    ):
+        inputs = ("a", "b", "bias") if bias else ("a", "b")
+        arguments = tuple(arg(name, "*fp16", "input", index=i) for i, name in enumerate(inputs)) + (
+            arg("output", "*fp16", "output", index=0),
+        ) + GEMM_DIMS + reserved()
+        constraints = ({"kind": "input_count_eq", "value": len(inputs)},) + GEMM_CONSTRAINTS
+        if bias:
+            constraints += ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)
+        register(KernelSpec(
+            kernel_id, op_type, 1, GEMM_SOURCE, arguments, GEMM_GRID, gemm_variants(prefix),
+            dtype="float16", constraints=constraints,
+        ))
+
+
+def register_elementwise() -> None:
+    # 8 halves per thread, 256 threads per workgroup.
+    for kernel_id, op_type, symbol, inputs in (
+        ("gelu.fp16.contiguous", "Gelu", "gelu_fp16", ("x",)),
+        ("add.fp16.contiguous", "Add", "add_fp16", ("a", "b")),
+    ):
+        arguments = tuple(arg(name, "*fp16", "input", index=i) for i, name in enumerate(inputs)) + (
+            arg("output", "*fp16", "output", index=0),
+            arg("total", "i32", "output_numel", index=0),
+        ) + reserved()
+        register(KernelSpec(
+            kernel_id, op_type, 1, "elementwise.hip", arguments, numel_grid(2048),
+            (KernelVariant("w4", symbol, num_warps=4, default=True),), dtype="float16",
+            constraints=({"kind": "input_count_eq", "value": len(inputs)},),
+        ))
+
+
+def register_norms() -> None:
+    for kernel_id, op_type, symbol, inputs in (
+        ("layer_norm.fp16.last_axis", "LayerNormalization", "layer_norm_fp16", ("x", "scale", "bias")),
+        ("skip_layer_norm.fp16.last_axis", "SkipLayerNormalization", "skip_layer_norm_fp16",
+         ("x", "residual", "scale", "bias")),
+    ):
+        arguments = tuple(arg(name, "*fp16", "input", index=i) for i, name in enumerate(inputs)) + (
+            arg("output", "*fp16", "output", index=0),
+            arg("rows", "i32", "input_dim", index=0, axis=0),
+            arg("columns", "i32", "input_dim", index=0, axis=1),
+            arg("epsilon", "fp32", "attribute_f64", name="epsilon", default=1e-5),
+        ) + reserved()
+        # One wavefront per row, four rows per workgroup.
+        register(KernelSpec(
+            kernel_id, op_type, 1, "layer_norm_fp16.hip", arguments,
+            (ceil_div(output_dim(0), literal(4)),),
+            (KernelVariant("wave_per_row", symbol, num_warps=4, default=True),),
+            dtype="float16",
+            constraints=(
+                {"kind": "input_count_eq", "value": len(inputs)},
+                {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+            ),
+        ))
+
+
+register_gemms()
+register_elementwise()
+register_norms()

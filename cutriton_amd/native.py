@@ -1,0 +1,82 @@
+"""Build and load the native pieces: the C++ engine library and the Kernel Pack.
+
+``build_all()`` compiles ``csrc/**/*.cc`` (host C++17 against the HIP runtime)
+into ``libcutriton_gfx950.so`` beside this file and runs the pack producer
+into ``pack/``. ``library()`` loads the engine library and raises when it is
+missing: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_DIR = PACKAGE_DIR.parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+INCLUDE_DIR = REPO_DIR / "include"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIBRARY_PATH = PACKAGE_DIR / "libcutriton_gfx950.so"
+PACK_DIR = PACKAGE_DIR / "pack"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+CXXFLAGS = (
+    "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra",
+    "-D__HIP_PLATFORM_AMD__",
+    f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", f"-I{ROCM / 'include'}",
+)
+
+
+def _compile(source: Path) -> Path:
+    obj = BUILD_DIR / (source.relative_to(CSRC_DIR).as_posix().replace("/", "_") + ".o")
+    cmd = ["g++", *CXXFLAGS, "-c", str(source), "-o", str(obj)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"g++ failed for {source}:\n{result.stderr}")
+    return obj
+
+
+def build_engine_library(jobs: int = 8) -> Path:
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC_DIR.rglob("*.cc"))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(_compile, sources))
+    staging = LIBRARY_PATH.with_suffix(".so.tmp")
+    cmd = ["g++", "-shared", "-o", str(staging), *map(str, objects),
+           f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stderr}")
+    os.replace(staging, LIBRARY_PATH)
+    return LIBRARY_PATH
+
+
+def build_kernel_pack(jobs: int = 8) -> Path:
+    cmd = ["python3", "-m", "cutriton_amd.kernel_sdk.builder", "--output", str(PACK_DIR), "--jobs", str(jobs)]
+    result = subprocess.run(cmd, cwd=REPO_DIR, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"kernel pack build failed:\n{result.stdout}\n{result.stderr}")
+    return PACK_DIR / "pack.json"
+
+
+def build_all(jobs: int = 8) -> None:
+    build_engine_library(jobs)
+    build_kernel_pack(jobs)
+
+
+_LIBRARY: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """The loaded engine library; raises if it was never built."""
+    global _LIBRARY
+    if _LIBRARY is None:
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(f"{LIBRARY_PATH} is missing: run __graft_entry__.build() first")
+        if not (PACK_DIR / "pack.json").exists():
+            raise RuntimeError(f"{PACK_DIR / 'pack.json'} is missing: run __graft_entry__.build() first")
+        _LIBRARY = ctypes.CDLL(str(LIBRARY_PATH))
+    return _LIBRARY

@@ -1,0 +1,88 @@
+// Engine (shared read-only state) and ExecutionContext (one run session).
+// Mirrors include/cutriton/runtime/engine.h:20-93 of the reference; the
+// device side is HIP: hipStream, hipEvent pairs and a hipGraph LRU.
+#pragma once
+
+#include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "cutriton/backend/backend.h"
+#include "cutriton/core/buffer.h"
+#include "cutriton/core/status.h"
+#include "cutriton/runtime/executable_plan.h"
+#include "cutriton/runtime/profiler.h"
+
+namespace cutriton {
+
+class ExecutionContext;
+class EngineState;
+
+class Engine {
+ public:
+  explicit Engine(ExecutablePlan plan);
+  const ExecutablePlan& plan() const;
+  // Each context owns its stream, workspace, profiler and graph cache.
+  std::unique_ptr<ExecutionContext> CreateExecutionContext() const;
+
+ private:
+  std::shared_ptr<EngineState> state_;
+};
+
+// Not thread-safe; at most one pending run at a time.
+class ExecutionContext {
+ public:
+  explicit ExecutionContext(std::shared_ptr<EngineState> state);
+  ~ExecutionContext();
+
+  // Name, shape, dtype, layout, device and buffer extent must match the plan.
+  Status BindInput(const std::string& name, Tensor tensor);
+  Status BindOutput(const std::string& name, Tensor tensor);
+  Status SelectShapeProfile(const std::string& name);
+  Status SetInputShape(const std::string& name, std::vector<int64_t> shape);
+  Status ResolveShapes();
+  const TensorDesc* GetResolvedTensorDesc(const std::string& name) const;
+  // RunAsync(nullptr) followed by Synchronize().
+  Status Run();
+  // Enqueues on `stream` (a hipStream_t), or on the context's own stream.
+  Status RunAsync(void* stream);
+  Status Synchronize();
+
+  const Profiler& profiler() const { return profiler_; }
+  std::size_t cached_hip_graph_count() const;
+  std::size_t loaded_hip_module_count() const;
+  const std::unordered_map<std::string, Tensor>& tensors() const { return tensors_; }
+  // Index of the chosen candidate per plan op (valid after the first run).
+  const std::vector<std::size_t>& selected_candidates() const { return selected_candidates_; }
+
+ private:
+  Status PrepareKernels();
+  Status PrepareTuning();
+  Status PrepareTensors();
+  Status ValidateBindings() const;
+  Status EnqueueOps(void* stream, bool capture);
+  Status CaptureGraph(void* stream, void** exec);
+  void InvalidateHipGraph();
+  const Graph& ActiveGraph() const;
+  const MemoryPlan& ActiveMemoryPlan() const;
+
+  std::shared_ptr<EngineState> state_;
+  bool kernels_prepared_{false};
+  bool tensors_prepared_{false};
+  bool run_pending_{false};
+  bool tuning_prepared_{false};
+  std::vector<std::size_t> selected_candidates_;
+  int selected_profile_{-1};
+  std::unordered_map<std::string, std::vector<int64_t>> input_shapes_;
+  Graph resolved_graph_;
+  bool shapes_resolved_{false};
+  std::vector<std::vector<std::unique_ptr<OpKernel>>> kernels_;
+  std::unordered_map<std::string, Tensor> tensors_;
+  std::shared_ptr<Buffer> workspace_;
+  Profiler profiler_;
+  // HIP stream/event/graph state; its type lives in the implementation.
+  void* hip_state_{nullptr};
+};
+
+}  // namespace cutriton

@@ -1,0 +1,257 @@
+"""Kernel-family parity on the GPU: every pack variant against the FP64 oracle.
+
+Each case builds a small graph, lowers it through the engine (a filtered
+pack pins the variant under test), runs it on cuda:0 through the C ABI and
+compares with oracle.evaluate on the same inputs.
+Tolerances: FP32 ops 1e-4 relative with a 1e-4*RMS floor; MaxPool and the
+Flatten view bit-exact; FP16 outputs 1e-2 absolute against FP64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cutriton_amd import engine, workloads
+from oracle import oracle
+from tests.helpers import assert_close_fp32, filtered_pack, only_variant, run_graph, without_kernels
+
+pytestmark = pytest.mark.gpu
+
+CONV_VARIANTS = ("m128n128", "m64n128", "m128n64", "m64n64")
+GEMM16_VARIANTS = ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64")
+
+
+def conv_graph(rng, n, c, h, w, k, r, stride, pad, dil, tail: str):
+    """Conv -> BatchNormalization [-> Relu | -> Add(residual) -> Relu]."""
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((n, c, h, w), "float32", "NCHW")
+    wt = rng.normal(0, np.sqrt(2.0 / (c * r * r)), (k, c, r, r)).astype(np.float32)
+    g.constant("w", wt, "OIHW")
+    names = []
+    for nm, arr in (("scale", rng.uniform(0.5, 1.5, k)), ("bias", rng.normal(0, 0.1, k)),
+                    ("mean", rng.normal(0, 0.1, k)), ("var", rng.uniform(0.5, 1.5, k))):
+        names.append(g.constant(nm, arr.astype(np.float32)))
+    y = g.add("conv", "Conv", ["x", "w"], ["conv_y"], strides=[stride, stride], pads=[pad] * 4,
+              dilations=[dil, dil])
+    feeds = {"x": rng.standard_normal((n, c, h, w), dtype=np.float32)}
+    if tail == "conv":
+        g.outputs.append(y)
+        return g, feeds
+    y = g.add("bn", "BatchNormalization", [y, *names], ["bn_y"], epsilon=1e-5)
+    if tail == "relu":
+        y = g.add("relu", "Relu", [y], ["out"])
+    elif tail == "add_relu":
+        oh = (h + 2 * pad - dil * (r - 1) - 1) // stride + 1
+        ow = (w + 2 * pad - dil * (r - 1) - 1) // stride + 1
+        g.inputs["res"] = ((n, k, oh, ow), "float32", "NCHW")
+        feeds["res"] = rng.standard_normal(g.inputs["res"][0], dtype=np.float32)
+        y = g.add("add", "Add", [y, "res"], ["sum"])
+        y = g.add("relu", "Relu", [y], ["out"])
+    g.outputs.append(y)
+    return g, feeds
+
+
+CONV_SHAPES = [
+    # n, c, h, w, k, r, stride, pad, dil
+    (1, 64, 56, 56, 64, 3, 1, 1, 1),     # the single-node configuration
+    (2, 36, 15, 13, 40, 3, 2, 1, 1),     # ragged tiles, stride 2, non-square
+    (2, 20, 7, 7, 72, 1, 1, 0, 1),       # 1x1, P*Q = 49 straddles tile columns
+    (1, 3, 31, 29, 16, 7, 2, 3, 1),      # stem-like: C*R*S = 147 (scalar weight loads)
+    (1, 8, 12, 12, 24, 3, 1, 2, 2),      # dilation 2
+]
+
+
+@pytest.mark.parametrize("variant", CONV_VARIANTS)
+@pytest.mark.parametrize("tail,kernel_id", [
+    ("relu", "conv_bn_relu.fp32.nchw.mfma"),
+    ("bn", "conv_bn.fp32.nchw.mfma"),
+    ("add_relu", "conv_bn_add_relu.fp32.nchw.mfma"),
+    ("conv", "conv.fp32.nchw.mfma"),
+])
+def test_conv_family_variants(tmp_path, variant, tail, kernel_id):
+    rng = np.random.default_rng(7)
+    pack = filtered_pack(tmp_path / "pack", only_variant(kernel_id, variant))
+    for shape in CONV_SHAPES:
+        g, feeds = conv_graph(rng, *shape, tail=tail)
+        opts = engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled")
+        out, eng, _ = run_graph(g, feeds, opts)
+        ops = eng.ops()
+        assert len(ops) == 1 and ops[0].candidates[ops[0].selected_candidate].endswith(f"{kernel_id}:{variant}"), ops
+        want = oracle.evaluate(g, feeds)[g.outputs[0]]
+        assert_close_fp32(out[g.outputs[0]], want, what=f"{kernel_id}:{variant} {shape}")
+
+
+@pytest.mark.parametrize("op", ["BatchNormalization", "Relu", "Add", "AddRelu"])
+@pytest.mark.parametrize("shape", [(2, 24, 9, 11), (1, 3, 5, 5), (32, 64, 56, 56)])
+def test_fp32_elementwise_kernels(op, shape):
+    """The unfused decomposition kernels (fusion.cpp:44-55 alternatives) as
+    single-op graphs; Add -> Relu fuses to AddRelu."""
+    rng = np.random.default_rng(11)
+    g = workloads.GraphSpec()
+    g.inputs["a"] = (shape, "float32", "NCHW")
+    feeds = {"a": rng.standard_normal(shape, dtype=np.float32)}
+    if op == "BatchNormalization":
+        c = shape[1]
+        names = [g.constant(nm, arr.astype(np.float32)) for nm, arr in (
+            ("scale", rng.uniform(0.5, 1.5, c)), ("bias", rng.normal(0, 0.1, c)),
+            ("mean", rng.normal(0, 0.1, c)), ("var", rng.uniform(0.5, 1.5, c)))]
+        g.add("bn", "BatchNormalization", ["a", *names], ["y"], epsilon=1e-5)
+    elif op == "Relu":
+        g.add("relu", "Relu", ["a"], ["y"])
+    else:
+        g.inputs["b"] = (shape, "float32", "NCHW")
+        feeds["b"] = rng.standard_normal(shape, dtype=np.float32)
+        y = g.add("add", "Add", ["a", "b"], ["s" if op == "AddRelu" else "y"])
+        if op == "AddRelu":
+            g.add("relu", "Relu", [y], ["y"])
+    g.outputs.append("y")
+    out, eng, _ = run_graph(g, feeds)
+    assert [o.op_type for o in eng.ops()] == [op]
+    assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"{op} {shape}")
+
+
+def test_tuner_runs_every_candidate(tmp_path):
+    """TuneOnMiss times every candidate of each op (fused variants and the
+    unfused decomposition) after checking it against candidate 0, writes one
+    cache file per op, and a second build reads the cache without rewriting."""
+    rng = np.random.default_rng(23)
+    g, feeds = conv_graph(rng, 2, 32, 14, 14, 64, 3, 1, 1, 1, tail="add_relu")
+    cache = tmp_path / "tuning"
+    opts = engine.CompileOptions(tuning_mode="tune_on_miss", tuning_cache_dir=str(cache),
+                                 tuning_warmup_iterations=1, tuning_measurement_iterations=3)
+    out, eng, ctx = run_graph(g, feeds, opts)
+    assert_close_fp32(out[g.outputs[0]], oracle.evaluate(g, feeds)[g.outputs[0]], what="tuned conv")
+    files = sorted(cache.glob("*.json"))
+    assert len(files) == 1
+    chosen = files[0].read_text()
+    assert any(c in chosen for c in eng.ops()[0].candidates)
+    stamp = files[0].stat().st_mtime_ns
+    out2, _, _ = run_graph(g, feeds, opts)
+    assert files[0].stat().st_mtime_ns == stamp
+    assert np.array_equal(out[g.outputs[0]], out2[g.outputs[0]])
+
+
+@pytest.mark.parametrize("variant", ("m64n64", "m128n128"))
+@pytest.mark.parametrize("m,k,n,bias", [(32, 2048, 1000, False), (5, 37, 29, True), (130, 64, 70, False),
+                                         (3, 2048, 1000, True)])
+def test_gemm_fp32(tmp_path, variant, m, k, n, bias):
+    rng = np.random.default_rng(3)
+    kid = "gemm_bias.fp32.mfma" if bias else "gemm.fp32.mfma"
+    pack = filtered_pack(tmp_path / "pack", only_variant(kid, variant))
+    g = workloads.GraphSpec()
+    g.inputs["a"] = ((m, k), "float32", "")
+    g.constant("b", rng.normal(0, 0.05, (k, n)).astype(np.float32))
+    ins = ["a", "b"]
+    if bias:
+        ins.append(g.constant("bias", rng.normal(0, 0.1, n).astype(np.float32)))
+    g.add("gemm", "Gemm", ins, ["y"])
+    g.outputs.append("y")
+    feeds = {"a": rng.standard_normal((m, k), dtype=np.float32)}
+    out, _, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"gemm fp32 {variant} {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("shape,kernel,stride,pad", [
+    ((2, 64, 112, 112), 3, 2, 1),   # ResNet stem pool
+    ((1, 5, 17, 14), 3, 2, 1),      # ragged
+    ((2, 3, 9, 9), 2, 2, 0),        # no padding, even window
+])
+def test_max_pool_bit_exact(shape, kernel, stride, pad):
+    rng = np.random.default_rng(5)
+    g = workloads.GraphSpec()
+    g.inputs["x"] = (shape, "float32", "NCHW")
+    g.add("pool", "MaxPool", ["x"], ["y"], kernel_shape=[kernel, kernel], strides=[stride, stride],
+          pads=[pad] * 4, dilations=[1, 1])
+    g.outputs.append("y")
+    feeds = {"x": rng.standard_normal(shape, dtype=np.float32)}
+    out, _, _ = run_graph(g, feeds)
+    want = oracle.evaluate(g, feeds)["y"].astype(np.float32)
+    assert np.array_equal(out["y"].view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(2, 2048, 7, 7), (3, 5, 1, 1), (1, 3, 60, 61), (1, 300, 8, 8)])
+def test_global_average_pool(shape):
+    rng = np.random.default_rng(9)
+    g = workloads.GraphSpec()
+    g.inputs["x"] = (shape, "float32", "NCHW")
+    g.add("gap", "GlobalAveragePool", ["x"], ["y"])
+    g.outputs.append("y")
+    feeds = {"x": rng.standard_normal(shape, dtype=np.float32)}
+    out, _, _ = run_graph(g, feeds)
+    assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"gap {shape}")
+
+
+def gemm16_graph(rng, m, k, n, gelu, bias):
+    g = workloads.GraphSpec()
+    g.inputs["a"] = ((m, k), "float16", "")
+    g.constant("b", rng.normal(0, 0.05, (k, n)).astype(np.float16))
+    ins = ["a", "b"]
+    if bias:
+        ins.append(g.constant("bias", rng.normal(0, 0.1, n).astype(np.float16)))
+    y = g.add("gemm", "Gemm", ins, ["h"])
+    if gelu:
+        y = g.add("gelu", "Gelu", [y], ["y"])
+    g.outputs.append(y)
+    return g, {"a": rng.standard_normal((m, k)).astype(np.float16)}
+
+
+@pytest.mark.parametrize("variant", GEMM16_VARIANTS)
+@pytest.mark.parametrize("gelu,bias", [(False, False), (True, False), (False, True), (True, True)])
+def test_gemm_fp16_variants(tmp_path, variant, gelu, bias):
+    rng = np.random.default_rng(13)
+    kid = {(False, False): "gemm.fp16.mfma", (True, False): "gemm_gelu.fp16.mfma",
+           (False, True): "gemm_bias.fp16.mfma", (True, True): "gemm_gelu_bias.fp16.mfma"}[(gelu, bias)]
+    pack = filtered_pack(tmp_path / "pack", only_variant(kid, variant))
+    for m, k, n in ((512, 768, 3072), (17, 128, 40), (70, 72, 37), (300, 200, 264)):
+        g, feeds = gemm16_graph(rng, m, k, n, gelu, bias)
+        out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+        ops = eng.ops()
+        assert len(ops) == 1 and ops[0].candidates[ops[0].selected_candidate].endswith(f"{kid}:{variant}"), ops
+        want = oracle.evaluate(g, feeds)[g.outputs[0]]
+        err = np.abs(out[g.outputs[0]].astype(np.float64) - want)
+        assert err.max() <= 1e-2, f"{kid}:{variant} {(m, k, n)} max abs err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("rows,cols", [(512, 768), (17, 100), (4, 5000), (64, 1024)])
+@pytest.mark.parametrize("skip", [False, True])
+def test_layer_norm_fp16(rows, cols, skip):
+    rng = np.random.default_rng(17)
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((rows, cols), "float16", "")
+    feeds = {"x": rng.standard_normal((rows, cols)).astype(np.float16)}
+    gamma = g.constant("gamma", rng.uniform(0.5, 1.5, cols).astype(np.float16))
+    beta = g.constant("beta", rng.normal(0, 0.1, cols).astype(np.float16))
+    y = "x"
+    if skip:
+        g.inputs["r"] = ((rows, cols), "float16", "")
+        feeds["r"] = rng.standard_normal((rows, cols)).astype(np.float16)
+        y = g.add("add", "Add", ["x", "r"], ["s"])
+    g.add("ln", "LayerNormalization", [y, gamma, beta], ["y"], axis=-1, epsilon=1e-5)
+    g.outputs.append("y")
+    out, eng, _ = run_graph(g, feeds)
+    assert [op.op_type for op in eng.ops()] == (["SkipLayerNormalization"] if skip else ["LayerNormalization"])
+    err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, feeds)["y"])
+    assert err.max() <= 1e-2, f"layer norm {rows}x{cols} skip={skip}: {err.max():.3e}"
+
+
+@pytest.mark.parametrize("op", ["Gelu", "Add"])
+@pytest.mark.parametrize("count", [(512, 3072), (3, 37)])
+def test_fp16_elementwise_kernels(op, count):
+    rng = np.random.default_rng(29)
+    g = workloads.GraphSpec()
+    g.inputs["a"] = (count, "float16", "")
+    feeds = {"a": (rng.standard_normal(count) * 2).astype(np.float16)}
+    if op == "Gelu":
+        g.add("gelu", "Gelu", ["a"], ["y"])
+    else:
+        g.inputs["b"] = (count, "float16", "")
+        feeds["b"] = rng.standard_normal(count).astype(np.float16)
+        g.add("add", "Add", ["a", "b"], ["y"])
+    g.outputs.append("y")
+    out, eng, _ = run_graph(g, feeds)
+    assert [o.op_type for o in eng.ops()] == [op]
+    want = oracle.evaluate(g, feeds)["y"]
+    # One FP16 rounding of an exact (Add) or FP32-accurate (Gelu) value.
+    err = np.abs(out["y"].astype(np.float64) - want)
+    assert np.all(err <= 2.0 ** -10 * np.abs(want) + 1e-6), err.max()

@@ -1,0 +1,85 @@
+"""Whole-graph parity on the GPU: ResNet-50 and the FP16 FFN through the
+engine (fused plan, hipGraph replay) against the FP64 oracle, plus the stem
+known-answer test of the reference (tests/cpp/test_cuda.cpp:444-479).
+
+Tolerances: ResNet-50 logits 1e-3 relative (norm-wise, and per element with
+a 1e-3*RMS floor); FFN outputs 1e-2 absolute; the stem KAT 1e-4 + 1e-4|e|
+as in the reference (test_cuda.cpp:168-180).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from cutriton_amd import engine, workloads
+from oracle import oracle
+from tests.helpers import assert_close_fp32, run_graph
+
+pytestmark = pytest.mark.gpu
+
+
+def test_stem_known_answer():
+    g, x, expected = workloads.stem_kat()
+    opts = engine.CompileOptions(tuning_mode="disabled", enable_profiling=True)
+    out, eng, ctx = run_graph(g, {"input": x}, opts, repeats=2)
+    got = out["output"].astype(np.float64)
+    assert np.all(np.abs(got - expected) <= 1e-4 + 1e-4 * np.abs(expected))
+    assert [op.op_type for op in eng.ops()] == ["FusedConvBatchNormRelu", "GlobalAveragePool", "Flatten", "Gemm"]
+    events = ctx.profile_events()
+    assert len(events) == 4 and events[2][1] == 0.0  # Flatten is a view and is not timed
+    assert ctx.cached_hip_graph_count() == 1
+
+
+def test_conv_bn_relu_single_node():
+    g, x = workloads.conv_bn_relu()
+    out, eng, _ = run_graph(g, {"x": x})
+    assert [op.op_type for op in eng.ops()] == ["FusedConvBatchNormRelu"]
+    assert_close_fp32(out[g.outputs[0]], oracle.evaluate(g, {"x": x})[g.outputs[0]], what="conv_bn_relu cfg0")
+
+
+def check_logits(got: np.ndarray, want: np.ndarray) -> None:
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel <= 1e-3, f"norm-wise relative error {rel:.3e}"
+    assert_close_fp32(got, want, rtol=1e-3, what="resnet50 logits")
+
+
+def test_resnet50_batch1():
+    g = workloads.resnet50(1)
+    x = workloads.resnet50_input(1)
+    out, eng, ctx = run_graph(g, {"input": x}, repeats=2)
+    ops = eng.ops()
+    assert len(ops) == 57
+    want = oracle.evaluate(g, {"input": x})["output"]
+    check_logits(out["output"].astype(np.float64), want)
+    assert ctx.cached_hip_graph_count() == 1
+
+
+def test_resnet50_batch32_matches_single_images():
+    """Batch invariance at the measured size: image i of a batch-32 run equals
+    the batch-1 run of that image (same kernels, same per-column arithmetic),
+    and images 0 and 31 also match the FP64 oracle."""
+    g32 = workloads.resnet50(32)
+    x = workloads.resnet50_input(32)
+    out32, _, _ = run_graph(g32, {"input": x}, repeats=2)
+    g1 = workloads.resnet50(1)
+    for i in (0, 31):
+        out1, _, _ = run_graph(g1, {"input": x[i:i + 1]})
+        assert_close_fp32(out32["output"][i:i + 1], out1["output"], rtol=1e-4, what=f"image {i}")
+        want = oracle.evaluate(g1, {"input": x[i:i + 1]})["output"]
+        check_logits(out32["output"][i:i + 1].astype(np.float64), want)
+
+
+def test_ffn_config_m512():
+    g, x = workloads.ffn(512, 768, 3072)
+    out, eng, _ = run_graph(g, {"x": x})
+    assert [op.op_type for op in eng.ops()] == ["GemmGelu", "Gemm", "SkipLayerNormalization"]
+    err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, {"x": x})["y"])
+    assert err.max() <= 1e-2, err.max()
+
+
+def test_ffn_config_m4096():
+    g, x = workloads.ffn(4096, 1024, 4096)
+    out, _, _ = run_graph(g, {"x": x})
+    err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, {"x": x})["y"])
+    assert err.max() <= 1e-2, err.max()
