@@ -7,13 +7,15 @@ Workloads (synthetic seeded inputs, random-init weights of the named shapes):
   * FP16 FFN block M=4096, H=1024, I=4096 (GemmGelu -> Gemm -> SkipLayerNorm):
     reported as TFLOP/s of its two GEMMs beside the main line.
 
-Timing: W untimed warm-up steps, then K steps bracketed by
-torch.cuda.synchronize(); each step is RunAsync on the measured stream +
-Synchronize, as in the reference harness (benchmarks/resnet50_native.cpp:281-291).
-Per-op HIP event pairs recorded inside the graph (the engine's profiler)
-give each kernel's duration over the same timed steps; the dominant kernel
-family (the FP32 implicit-GEMM convolutions) is priced against the FP32
-MFMA peak from those durations.
+Timing: the first run tunes every op (TuneOnMiss, cache in a temporary
+directory). Then W untimed warm-up steps and K timed steps bracketed by
+torch.cuda.synchronize(), on an engine built from that cache with profiling
+off; each step is RunAsync on the measured stream + Synchronize, as in the
+reference harness (benchmarks/resnet50_native.cpp:281-291). A second set of K
+steps on a profiled engine (per-op HIP event pairs recorded inside the graph)
+gives each kernel's duration; the dominant kernel family (the FP32
+implicit-GEMM convolutions) is priced against the FP32 MFMA peak from those
+durations.
 
 The CPU baseline is the reference's CPU path (the same graph in PyTorch-CPU
 FP32, oracle/torch_cpu.py) on a bounded sample, timed on this host.
@@ -37,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "ResNet-50 fp32 img/s @bs32 (% FP32 MFMA peak); FFN fp16 TFLOP/s @M=4096"
 FP32_MFMA_PEAK_TFLOPS = 157.3
 FP16_MFMA_PEAK_TFLOPS = 2516.6
+KERNEL_TIMING_LAUNCHES = 20
 CONV_OPS = ("FusedConvBatchNormRelu", "FusedConvBatchNorm", "FusedConvBatchNormAddRelu", "Conv")
 
 
@@ -44,15 +47,13 @@ def log(*args) -> None:
     print(*args, file=sys.stderr, flush=True)
 
 
-def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiling: bool):
-    """Builds and tunes `graph`, then times `steps` steps. Returns
-    (ms per step list, per-op total ms over the timed steps, plan ops)."""
+def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str):
     import numpy as np
     import torch
 
     from cutriton_amd import engine, workloads
 
-    opts = engine.CompileOptions(tuning_mode="tune_on_miss", tuning_cache_dir=cache_dir,
+    opts = engine.CompileOptions(tuning_mode=tuning_mode, tuning_cache_dir=cache_dir,
                                  enable_profiling=profiling, enable_hip_graph=True,
                                  tuning_warmup_iterations=3, tuning_measurement_iterations=10)
     eng = engine.build_engine(workloads.to_model(graph), opts)
@@ -65,8 +66,25 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profilin
         shape, dtype = eng.value_desc(name)
         outputs[name] = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
         ctx.bind_output(name, outputs[name], layout="NCHW" if len(shape) == 4 else "")
+    return eng, ctx, (inputs, outputs)
+
+
+def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str):
+    """Tunes `graph` (TuneOnMiss), then:
+      1. a profiled engine replays `steps` steps and sums each op's HIP-event
+         duration (kernel time, read from the event nodes inside the graph);
+      2. an unprofiled engine built from the tuning cache (UseCache) replays
+         `steps` steps bracketed by device synchronisation: the wall time of
+         these is the step time.
+      3. each op's selected kernels are timed over back-to-back launches on
+         the measured stream (ExecutionContext::TimeOp).
+    Returns (ms per step, per-op kernel ms, per-op graph-event ms per step,
+    plan ops, selected candidate per op)."""
+    import torch
+
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
+    eng, ctx, keep = _context(graph, feeds, cache_dir, True, "tune_on_miss")
     t0 = time.perf_counter()
     ctx.run_async(handle)  # first run: tuning, module loads, graph capture
     ctx.synchronize()
@@ -76,23 +94,52 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profilin
         ctx.synchronize()
     ops = eng.ops()
     op_ms = [0.0] * len(ops)
-    step_ms = []
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(steps):
+        ctx.run_async(handle)
+        ctx.synchronize()
+        for i, (_, ms) in enumerate(ctx.profile_events()):
+            op_ms[i] += ms
+    selected = [op.candidates[s] for op, s in zip(ops, ctx.selected_candidates(len(ops)))]
+    del ctx, eng, keep
+
+    eng, ctx, keep = _context(graph, feeds, cache_dir, False, "use_cache")
+    ctx.run_async(handle)
+    ctx.synchronize()
+    plain = [op.candidates[s] for op, s in zip(eng.ops(), ctx.selected_candidates(len(ops)))]
+    if plain != selected:
+        raise RuntimeError("the tuning cache did not reproduce the tuned plan")
+    for _ in range(warmup):
+        ctx.run_async(handle)
+        ctx.synchronize()
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for _ in range(steps):
-        start.record(stream)
         ctx.run_async(handle)
-        end.record(stream)
         ctx.synchronize()
-        step_ms.append(start.elapsed_time(end))
-        if profiling:
-            for i, (_, ms) in enumerate(ctx.profile_events()):
-                op_ms[i] += ms
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - wall0) * 1e3
-    selected = [op.candidates[s] for op, s in zip(ops, ctx.selected_candidates(len(ops)))]
-    return step_ms, wall_ms, op_ms, ops, selected
+    ms_per_step = (time.perf_counter() - wall0) * 1e3 / steps
+    # Kernel time per op on the same stream: back-to-back launches between
+    # one event pair, free of the event nodes' dispatch gaps.
+    kernel_ms = [ctx.time_op(i, KERNEL_TIMING_LAUNCHES, handle) for i in range(len(ops))]
+    graph_event_ms = [v / steps for v in op_ms]
+    return ms_per_step, kernel_ms, graph_event_ms, ops, selected
+
+
+TRAFFIC_SUMMARY = ROOT / "profiles" / "resnet50_bs32_fp32_hbm_traffic.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per conv-family launch from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter
+    on a copy of known size). Counters need rocprofv3 around the process, so
+    the figure is read from that summary, not measured in this run."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("conv_family_hbm_bytes_per_launch ="):
+                return int(line.split("=", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def bench_resnet(args, cache_dir: str) -> dict:
@@ -101,23 +148,28 @@ def bench_resnet(args, cache_dir: str) -> dict:
     batch = 32
     graph = workloads.resnet50(batch)
     x = workloads.resnet50_input(batch)
-    step_ms, wall_ms, op_ms, ops, selected = run_workload(graph, {"input": x}, args.steps, args.warmup,
-                                                         cache_dir, profiling=True)
+    ms_per_step, kernel_ms, event_ms, ops, selected = run_workload(graph, {"input": x}, args.steps, args.warmup,
+                                                                   cache_dir)
     flops = workloads.node_flops(graph)
     conv_flops = sum(v for k, v in flops.items() if k != "classifier")
     total_flops = sum(flops.values())
-    ms_per_step = wall_ms / args.steps
     img_s = batch * 1e3 / ms_per_step
     conv_idx = [i for i, op in enumerate(ops) if op.op_type in CONV_OPS]
-    conv_ms = sum(op_ms[i] for i in conv_idx) / args.steps
+    conv_ms = sum(kernel_ms[i] for i in conv_idx)
     launches = len(conv_idx)
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
-    per_op = sorted(((op_ms[i] / args.steps, ops[i].node_name, selected[i].split(":")[-1]) for i in range(len(ops))),
-                    reverse=True)
-    log(f"  resnet50 bs32: {ms_per_step:.3f} ms/step (event median {sorted(step_ms)[len(step_ms) // 2]:.3f}), "
-        f"{img_s:.1f} img/s, conv kernels {conv_ms:.3f} ms/step")
-    for ms, name, var in per_op[:12]:
-        log(f"    {ms * 1e3:8.1f} us  {name}  [{var}]")
+
+    def op_flops(name: str) -> int:
+        keys = [k for k in flops if name.startswith(k)]
+        return flops[max(keys, key=len)] if keys else 0
+
+    per_op = sorted(((kernel_ms[i], ops[i].node_name, selected[i].split(":", 1)[-1], op_flops(ops[i].node_name))
+                     for i in range(len(ops))), reverse=True)
+    log(f"  resnet50 bs32: {ms_per_step:.3f} ms/step, {img_s:.1f} img/s; kernel time per step: conv "
+        f"{conv_ms:.3f} ms, all {sum(kernel_ms):.3f} ms (profiled graph events {sum(event_ms):.3f} ms)")
+    for ms, name, var, fl in per_op:
+        rate = f"{fl / (ms * 1e-3) / 1e12:6.1f} TF/s" if fl and ms > 0 else " " * 11
+        log(f"    {ms * 1e3:8.1f} us {rate}  {name}  [{var}]")
     return {
         "ms_per_step": ms_per_step,
         "img_s": img_s,
@@ -130,9 +182,12 @@ def bench_resnet(args, cache_dir: str) -> dict:
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": f"{TRAFFIC_SUMMARY.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
             "flop_per_launch": conv_flops / launches,
+            "launches_per_step": launches,
             "avg_launch_us": conv_ms * 1e3 / launches,
+            "timing": f"ExecutionContext::TimeOp, {KERNEL_TIMING_LAUNCHES} back-to-back launches per op, HIP events",
         },
         "selected": selected,
     }
@@ -143,11 +198,9 @@ def bench_ffn(args, cache_dir: str) -> dict:
 
     m, h, i = 4096, 1024, 4096
     graph, x = workloads.ffn(m, h, i)
-    step_ms, wall_ms, op_ms, ops, selected = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir,
-                                                         profiling=True)
+    ms_per_step, kernel_ms, _, ops, selected = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir)
     gemm_flops = 2 * m * h * i
-    per_op = {op.op_type: op_ms[j] / args.steps for j, op in enumerate(ops)}
-    ms_per_step = wall_ms / args.steps
+    per_op = {op.op_type: kernel_ms[j] for j, op in enumerate(ops)}
     out = {
         "workload": f"ffn_fp16_m{m}_h{h}_i{i}",
         "ms_per_step": ms_per_step,
@@ -165,6 +218,29 @@ def bench_ffn(args, cache_dir: str) -> dict:
     log(f"  ffn: {ms_per_step * 1e3:.1f} us/step; GemmGelu {out['gemm_gelu_us']:.1f} us "
         f"({out['gemm_gelu_tflops']:.0f} TF), Gemm {out['gemm_us']:.1f} us ({out['gemm_tflops']:.0f} TF), "
         f"SkipLN {out['skip_layer_norm_us']:.1f} us")
+    return out
+
+
+def bench_copy(args, cache_dir: str) -> dict:
+    """One Relu over 64 Mi non-negative floats: the relu_fp32 kernel reads and
+    writes exactly 256 MiB each. Its GB/s is the streaming reference for the
+    bandwidth kernels, and its FETCH_SIZE / WRITE_SIZE counters calibrate the
+    HBM traffic figures of the other kernels."""
+    import numpy as np
+
+    from cutriton_amd import workloads
+
+    count = 64 << 20
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((count,), "float32", "")
+    g.add("copy", "Relu", ["x"], ["y"])
+    g.outputs.append("y")
+    x = np.abs(np.random.default_rng(workloads.SEED).standard_normal(count, dtype=np.float32))
+    ms_per_step, op_kernel_ms, _, ops, _ = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    kernel_ms = op_kernel_ms[0]
+    out = {"workload": "relu_fp32_64Mi", "bytes": 2 * 4 * count, "kernel_us": kernel_ms * 1e3,
+           "gbps": 2 * 4 * count / (kernel_ms * 1e-3) / 1e9, "ms_per_step": ms_per_step}
+    log(f"  copy: {out['kernel_us']:.1f} us, {out['gbps']:.0f} GB/s")
     return out
 
 
@@ -214,7 +290,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=("all", "resnet50", "ffn"), default="all")
+    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "copy"), default="all")
+    parser.add_argument("--tuning-cache", default="",
+                        help="tuning cache folder to reuse (default: a fresh temporary folder, so every op is tuned)")
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                         help="bounded CPU sample; 0 skips the CPU baseline")
     args = parser.parse_args()
@@ -228,7 +306,8 @@ def main() -> int:
         print("bench.py needs a GPU (cuda:0)", file=sys.stderr)
         return 2
     log(f"device: {torch.cuda.get_device_name(0)}")
-    cache_dir = tempfile.mkdtemp(prefix="cutriton-tuning-")
+    cache_dir = args.tuning_cache or tempfile.mkdtemp(prefix="cutriton-tuning-")
+    os.makedirs(cache_dir, exist_ok=True)
     result = {
         "metric": METRIC, "value": None, "unit": "img/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
@@ -248,6 +327,10 @@ def main() -> int:
         if args.workload == "ffn":
             result.update(value=round(f["tflops_block"], 3), unit="TFLOP/s", ms_per_step=round(f["ms_per_step"], 4),
                           dtype="fp16", config={"workload": f["workload"], "parallelism": "single-gpu"})
+    if args.workload == "copy":
+        c = bench_copy(args, cache_dir)
+        result.update(value=round(c["gbps"], 1), unit="GB/s", ms_per_step=round(c["ms_per_step"], 4),
+                      config={"workload": c["workload"], "parallelism": "single-gpu"}, copy=c)
     if args.cpu_baseline_seconds > 0 and args.workload in ("all", "resnet50"):
         result["cpu_baseline"] = cpu_baseline(args.cpu_baseline_seconds)
     print(json.dumps(result), flush=True)

@@ -126,6 +126,7 @@ Status BindArguments(const KernelInvocation& invocation, const KernelContext& co
                      std::vector<ArgumentSlot>* slots) {
   slots->assign(invocation.artifact.arguments.size(), ArgumentSlot{nullptr});
   const Node& node = *context.node;
+  bool scratch_bound = false;
   for (std::size_t i = 0; i < invocation.artifact.arguments.size(); ++i) {
     const KernelArgumentSource& s = invocation.artifact.arguments[i].source;
     ArgumentSlot& slot = (*slots)[i];
@@ -189,6 +190,16 @@ Status BindArguments(const KernelInvocation& invocation, const KernelContext& co
         break;
       case KernelArgumentSourceKind::kRuntimeReserved:
         slot.pointer = nullptr;
+        if (invocation.artifact.runtime_scratch_bytes > 0 && !scratch_bound) {
+          if (context.runtime_scratch == nullptr ||
+              context.runtime_scratch_bytes < static_cast<std::size_t>(invocation.artifact.runtime_scratch_bytes)) {
+            return Status::RuntimeError("kernel " + invocation.artifact.symbol + " needs " +
+                                        std::to_string(invocation.artifact.runtime_scratch_bytes) +
+                                        " bytes of runtime scratch");
+          }
+          slot.pointer = context.runtime_scratch;
+          scratch_bound = true;
+        }
         break;
     }
   }

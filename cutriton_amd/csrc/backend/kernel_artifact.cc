@@ -235,6 +235,11 @@ Status ArtifactRepository::Load(const std::vector<std::string>& paths) {
         a.num_warps = AsInt(entry.at("num_warps"));
         a.num_stages = AsInt(entry.at("num_stages"));
         a.shared_memory_bytes = AsInt(entry.at("shared_memory_bytes"));
+        if (const Value* scratch = entry.find("runtime_scratch_bytes")) {
+          const double bytes = scratch->number();
+          if (bytes < 0 || bytes > 1e12) throw std::runtime_error("runtime_scratch_bytes is out of range");
+          a.runtime_scratch_bytes = static_cast<std::int64_t>(bytes);
+        }
         if (a.num_warps <= 0 || a.num_warps > 16) {
           throw std::runtime_error("num_warps must be in 1..16 wavefronts");
         }

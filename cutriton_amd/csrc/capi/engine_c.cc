@@ -393,4 +393,9 @@ int ct_context_selected_candidate(const ct_context* context, int op_index) {
              : static_cast<int>(selected[static_cast<std::size_t>(op_index)]);
 }
 
+int ct_context_time_op(ct_context* context, int op_index, int iterations, void* stream, double* ms_per_launch) {
+  if (context == nullptr || op_index < 0) return Invalid("null context or negative op index");
+  return Report(context->context->TimeOp(static_cast<std::size_t>(op_index), iterations, stream, ms_per_launch));
+}
+
 }  // extern "C"

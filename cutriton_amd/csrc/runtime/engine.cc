@@ -23,6 +23,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
@@ -518,6 +520,25 @@ Status ExecutionContext::PrepareTensors() {
     }
     tensors_[allocation.value_name] = Tensor(value->tensor, workspace_, allocation.offset);
   }
+  // One zero-initialised runtime scratch buffer per context, sized for the
+  // largest declared need of any candidate (tuning may run every one).
+  std::int64_t scratch = 0;
+  for (const auto& op : state_->plan.ops()) {
+    for (const auto& candidate : op.candidates) {
+      for (const auto& step : candidate.steps) {
+        if (const auto* inv = std::get_if<KernelInvocation>(&step)) {
+          scratch = std::max(scratch, inv->artifact.runtime_scratch_bytes);
+        }
+      }
+    }
+  }
+  if (scratch > 0 && device.type == DeviceType::kHIP &&
+      (runtime_scratch_ == nullptr || runtime_scratch_->size_bytes() < static_cast<std::size_t>(scratch))) {
+    CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(static_cast<std::size_t>(scratch), device.id, &runtime_scratch_));
+    CUTRITON_RETURN_IF_ERROR(RuntimeStatus(
+        cth_memset(runtime_scratch_->data(), 0, runtime_scratch_->size_bytes(), device.id), "hipMemset"));
+    InvalidateHipGraph();
+  }
   tensors_prepared_ = true;
   return Status::OK();
 }
@@ -649,18 +670,22 @@ Status ExecutionContext::PrepareTuning() {
     const Node& node = graph.nodes().at(static_cast<std::size_t>(ops[i].node_id));
     std::vector<std::unique_ptr<OpKernel>> kernels;
     CUTRITON_RETURN_IF_ERROR(build_kernels(ops[i].candidates[selected_candidates_[i]], &kernels));
-    KernelContext context{&node, &tensors_, stream, nullptr};
+    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
     for (auto& kernel : kernels) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
   }
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(stream), "hipStreamSynchronize"));
 
+  // CUTRITON_TUNING_LOG=1 prints every candidate's median and every
+  // numeric-gate rejection to stderr.
+  const bool tuning_log = std::getenv("CUTRITON_TUNING_LOG") != nullptr;
   for (const std::size_t op_index : to_tune) {
     const PlanOp& op = ops[op_index];
     const Node& node = graph.nodes().at(static_cast<std::size_t>(op.node_id));
-    KernelContext context{&node, &tensors_, stream, nullptr};
+    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
     double best_ms = std::numeric_limits<double>::infinity();
     std::size_t best = op.selected_candidate;
     std::vector<float> reference;
+    float reference_rms = 0.0f;
     for (std::size_t c = 0; c < op.candidates.size(); ++c) {
       std::vector<std::unique_ptr<OpKernel>> kernels;
       CUTRITON_RETURN_IF_ERROR(build_kernels(op.candidates[c], &kernels));
@@ -674,14 +699,29 @@ Status ExecutionContext::PrepareTuning() {
       CUTRITON_RETURN_IF_ERROR(TensorToHostFloats(output, &produced));
       if (reference.empty()) {
         reference = std::move(produced);
+        double sum_sq = 0.0;
+        for (const float v : reference) sum_sq += static_cast<double>(v) * v;
+        reference_rms = reference.empty() ? 0.0f : static_cast<float>(std::sqrt(sum_sq / reference.size()));
       } else {
+        // Candidates differ only in summation order, so an element may
+        // differ by a relative amount of the output's scale, not of its own
+        // value: the absolute floor is rel * max(1, rms of the output).
         const float rel = output.desc().dtype == DataType::kFloat16 ? 1e-2f : 1e-4f;
+        const float floor = rel * std::max(1.0f, reference_rms);
         bool agrees = true;
-        for (std::size_t e = 0; e < produced.size() && agrees; ++e) {
-          const float tolerance = rel + rel * std::fabs(reference[e]);
+        std::size_t e = 0;
+        for (; e < produced.size() && agrees; ++e) {
+          const float tolerance = floor + rel * std::fabs(reference[e]);
           agrees = std::isfinite(produced[e]) && std::fabs(produced[e] - reference[e]) <= tolerance;
         }
-        if (!agrees) continue;
+        if (!agrees) {
+          if (tuning_log) {
+            std::fprintf(stderr, "[cutriton tuning] %s: %s rejected (element %zu: %g vs %g)\n",
+                         op.node_name.c_str(), op.candidates[c].candidate_id.c_str(), e - 1,
+                         static_cast<double>(produced[e - 1]), static_cast<double>(reference[e - 1]));
+          }
+          continue;
+        }
       }
       std::vector<float> samples;
       for (int it = 0; it < std::max(1, config.measurement_iterations); ++it) {
@@ -695,6 +735,10 @@ Status ExecutionContext::PrepareTuning() {
       }
       std::sort(samples.begin(), samples.end());
       const double median = samples[samples.size() / 2];
+      if (tuning_log) {
+        std::fprintf(stderr, "[cutriton tuning] %s: %s %.4f ms\n", op.node_name.c_str(),
+                     op.candidates[c].candidate_id.c_str(), median);
+      }
       if (median < best_ms) {
         best_ms = median;
         best = c;
@@ -750,7 +794,7 @@ Status ExecutionContext::EnqueueOps(void* stream, bool capture) {
     // Events inside a capture are graph nodes placed by CaptureGraph.
     events.timed = profiling && node.op_type() != "Flatten";
     if (events.timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(events.start, stream), "hipEventRecord"));
-    KernelContext context{&node, &tensors_, stream, nullptr};
+    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
     for (auto& kernel : kernels_[i]) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
     if (events.timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(events.end, stream), "hipEventRecord"));
   }
@@ -794,7 +838,7 @@ Status ExecutionContext::CaptureGraph(void* stream, void** exec) {
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_graph_add_event_record(parent, previous, events.start, &previous),
                                            "hipGraphAddEventRecordNode"));
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_begin_capture(stream), "hipStreamBeginCapture"));
-    KernelContext context{&node, &tensors_, stream, nullptr};
+    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
     Status launched = Status::OK();
     for (auto& kernel : kernels_[i]) {
       launched = kernel->Compute(&context);
@@ -831,7 +875,7 @@ Status ExecutionContext::RunAsync(void* stream) {
       const PlanOp& op = state_->plan.ops()[i];
       const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
       KernelContext context{&node, &tensors_, stream,
-                            state_->plan.enable_profiling() ? &profiler_ : nullptr};
+                            state_->plan.enable_profiling() ? &profiler_ : nullptr, ScratchPointer(), ScratchBytes()};
       for (auto& kernel : kernels_[i]) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
     }
     run_pending_ = true;
@@ -887,6 +931,44 @@ Status ExecutionContext::RunAsync(void* stream) {
   entry->last_used = ++hip->clock;
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_graph_launch(entry->exec, hip->active_stream), "hipGraphLaunch"));
   run_pending_ = true;
+  return Status::OK();
+}
+
+Status ExecutionContext::TimeOp(std::size_t op_index, int iterations, void* stream, double* ms_per_launch) {
+  if (ms_per_launch == nullptr || iterations < 1) return Status::InvalidArgument("TimeOp needs iterations >= 1");
+  if (run_pending_) return Status::RuntimeError("TimeOp while a run is pending");
+  auto* hip = static_cast<HipExecutionState*>(hip_state_);
+  if (!kernels_prepared_ || hip == nullptr) return Status::RuntimeError("TimeOp needs a completed HIP run first");
+  if (op_index >= kernels_.size()) return Status::InvalidArgument("TimeOp: op index out of range");
+  *ms_per_launch = 0.0;
+  const PlanOp& op = state_->plan.ops()[op_index];
+  const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
+  // Flatten is a view: no launch, not timed (as in the profiled graph).
+  if (kernels_[op_index].empty() || node.op_type() == "Flatten") return Status::OK();
+  void* s = stream == nullptr ? hip->owned_stream : stream;
+  KernelContext context{&node, &tensors_, s, nullptr, ScratchPointer(), ScratchBytes()};
+  cth_event start = nullptr;
+  cth_event end = nullptr;
+  CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_set_device(state_->plan.backend_options().device.id), "hipSetDevice"));
+  CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_create(&start), "hipEventCreate"));
+  Status status = RuntimeStatus(cth_event_create(&end), "hipEventCreate");
+  for (auto& kernel : kernels_[op_index]) {
+    if (status.ok()) status = kernel->Compute(&context);
+  }
+  if (status.ok()) status = RuntimeStatus(cth_event_record(start, s), "hipEventRecord");
+  for (int it = 0; it < iterations && status.ok(); ++it) {
+    for (auto& kernel : kernels_[op_index]) {
+      if (status.ok()) status = kernel->Compute(&context);
+    }
+  }
+  if (status.ok()) status = RuntimeStatus(cth_event_record(end, s), "hipEventRecord");
+  if (status.ok()) status = RuntimeStatus(cth_event_synchronize(end), "hipEventSynchronize");
+  float ms = 0.0f;
+  if (status.ok()) status = RuntimeStatus(cth_event_elapsed_ms(&ms, start, end), "hipEventElapsedTime");
+  cth_event_destroy(start);
+  if (end != nullptr) cth_event_destroy(end);
+  CUTRITON_RETURN_IF_ERROR(status);
+  *ms_per_launch = static_cast<double>(ms) / iterations;
   return Status::OK();
 }
 

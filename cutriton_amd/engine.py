@@ -94,6 +94,7 @@ def _lib() -> ctypes.CDLL:
         "ct_context_profile_event": (I, [P, I, C, S, ctypes.POINTER(D)]),
         "ct_context_graph_count": (S, [P]),
         "ct_context_module_count": (S, [P]),
+        "ct_context_time_op": (I, [P, I, I, P, ctypes.POINTER(D)]),
         "ct_context_selected_candidate": (I, [P, I]),
     }
     for name, (restype, argtypes) in sigs.items():
@@ -381,6 +382,13 @@ class ExecutionContext:
 
     def loaded_hip_module_count(self) -> int:
         return self._lib.ct_context_module_count(self.handle)
+
+    def time_op(self, op_index: int, iterations: int = 20, stream: int | None = None) -> float:
+        """Milliseconds per launch of plan op `op_index`'s selected kernels,
+        timed over `iterations` back-to-back launches (needs a completed run)."""
+        ms = ctypes.c_double()
+        _check(self._lib.ct_context_time_op(self.handle, op_index, iterations, stream, ctypes.byref(ms)))
+        return ms.value
 
     def selected_candidates(self, count: int) -> list[int]:
         return [self._lib.ct_context_selected_candidate(self.handle, i) for i in range(count)]

@@ -89,7 +89,7 @@ def elf_function_symbols(image: bytes) -> set[str]:
 def _entries(spec: KernelSpec, binary: str, digest: str) -> list[dict[str, Any]]:
     arguments = [{"name": a.name, "type": a.type, "source": a.source} for a in spec.arguments]
     grid = list(spec.grid) + [{"kind": "literal", "value": 1}] * (3 - len(spec.grid))
-    return [
+    entries = [
         {
             "kernel_id": spec.kernel_id,
             "op_type": spec.op_type,
@@ -114,6 +114,10 @@ def _entries(spec: KernelSpec, binary: str, digest: str) -> list[dict[str, Any]]
         }
         for v in spec.variants
     ]
+    for entry, v in zip(entries, spec.variants):
+        if v.scratch_bytes:
+            entry["runtime_scratch_bytes"] = v.scratch_bytes
+    return entries
 
 
 def build_pack(output: Path, modules: tuple[str, ...] = DEFAULT_MODULES, jobs: int = 8) -> Path:

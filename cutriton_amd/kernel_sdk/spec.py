@@ -72,6 +72,9 @@ class KernelVariant:
     num_stages: int = 1
     meta: dict[str, int] = field(default_factory=dict)
     default: bool = False
+    # Bytes of zero-initialised device scratch bound to the first
+    # runtime_reserved argument (0: that argument stays null).
+    scratch_bytes: int = 0
 
 
 @dataclass(frozen=True)
@@ -103,6 +106,8 @@ class KernelSpec:
                 raise ValueError(f"{self.kernel_id}: variant symbol is not a C identifier")
             if not 1 <= variant.num_warps <= 16:
                 raise ValueError(f"{self.kernel_id}: num_warps must be 1..16 wavefronts")
+            if not isinstance(variant.scratch_bytes, int) or variant.scratch_bytes < 0:
+                raise ValueError(f"{self.kernel_id}: scratch_bytes must be a non-negative integer")
             if any(not name or not isinstance(value, int) or value <= 0 for name, value in variant.meta.items()):
                 raise ValueError(f"{self.kernel_id}: variant meta must be positive integers")
         names = [argument.name for argument in self.arguments]

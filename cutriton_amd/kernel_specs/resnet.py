@@ -29,9 +29,10 @@ CONV_SOURCE = "conv_fp32.hip"
 # (variant id, BLOCK_M, BLOCK_N, BLOCK_K); BLOCK_M tiles output channels and
 # BLOCK_N tiles (image, output pixel) columns.
 CONV_TILES = (
-    ("m128n128", 128, 128, 16),
+    ("m128n128", 128, 128, 32),
+    ("m64n256", 64, 256, 16),
     ("m64n128", 64, 128, 32),
-    ("m128n64", 128, 64, 16),
+    ("m128n64", 128, 64, 32),
     ("m64n64", 64, 64, 32),
 )
 CONV_DEFAULT = "m128n128"
@@ -74,6 +75,23 @@ def conv_variants(prefix: str) -> tuple[KernelVariant, ...]:
     )
 
 
+# Register-direct variants (conv_direct_fp32.hip): (variant id, BLOCK_M, BLOCK_N).
+DIRECT_SOURCE = "conv_direct_fp32.hip"
+DIRECT_TILES = (
+    ("d64n256", 64, 256),
+    ("d64n64", 64, 64),
+    ("d32n64", 32, 64),
+)
+DIRECT_DEFAULT = "d64n64"
+
+def direct_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return tuple(
+        KernelVariant(name, f"{prefix}_{name}", num_warps=4, meta={"BLOCK_M": bm, "BLOCK_N": bn},
+                      default=name == DIRECT_DEFAULT)
+        for name, bm, bn in DIRECT_TILES
+    )
+
+
 def register_conv_family() -> None:
     bn_inputs = tuple(
         arg(name, "*fp32", "input", index=i)
@@ -81,35 +99,39 @@ def register_conv_family() -> None:
     )
     epsilon = arg("epsilon", "fp32", "attribute_f64", name="batchnorm_epsilon", default=1e-5)
     for op_type, kernel_id, prefix, inputs in (
-        ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw.mfma", "conv_bn_relu_fp32", bn_inputs),
-        ("FusedConvBatchNorm", "conv_bn.fp32.nchw.mfma", "conv_bn_fp32", bn_inputs),
+        ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw", "conv_bn_relu_fp32", bn_inputs),
+        ("FusedConvBatchNorm", "conv_bn.fp32.nchw", "conv_bn_fp32", bn_inputs),
         (
             "FusedConvBatchNormAddRelu",
-            "conv_bn_add_relu.fp32.nchw.mfma",
+            "conv_bn_add_relu.fp32.nchw",
             "conv_bn_add_relu_fp32",
             bn_inputs + (arg("residual", "*fp32", "input", index=6),),
         ),
     ):
         arguments = inputs + (arg("output", "*fp32", "output", index=0),) + CONV_DIMENSIONS + (epsilon,) + reserved()
-        register(KernelSpec(
-            kernel_id, op_type, 1, CONV_SOURCE, arguments, CONV_GRID, conv_variants(prefix),
-            layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},),
-        ))
+        for source, suffix, variants, grid in ((CONV_SOURCE, "mfma", conv_variants(prefix), CONV_GRID),
+                                               (DIRECT_SOURCE, "direct", direct_variants(prefix), CONV_GRID)):
+            register(KernelSpec(
+                f"{kernel_id}.{suffix}", op_type, 1, source, arguments, grid, variants,
+                layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},),
+            ))
     conv_arguments = (
         arg("x", "*fp32", "input", index=0),
         arg("weight", "*fp32", "input", index=1),
         arg("output", "*fp32", "output", index=0),
     ) + CONV_DIMENSIONS + reserved()
-    register(KernelSpec(
-        "conv.fp32.nchw.mfma", "Conv", 1, CONV_SOURCE, conv_arguments, CONV_GRID, conv_variants("conv_fp32"),
-        layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},),
-    ))
+    for source, suffix, variants, grid in ((CONV_SOURCE, "mfma", conv_variants("conv_fp32"), CONV_GRID),
+                                           (DIRECT_SOURCE, "direct", direct_variants("conv_fp32"), CONV_GRID)):
+        register(KernelSpec(
+            f"conv.fp32.nchw.{suffix}", "Conv", 1, source, conv_arguments, grid, variants,
+            layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},),
+        ))
 
 
 def register_gemm() -> None:
     # C[M,N] = A[M,K] B[K,N]: x = ceil(N / BLOCK_N), y = ceil(M / BLOCK_M).
     grid = (ceil_div(output_dim(1), meta("BLOCK_N")), ceil_div(output_dim(0), meta("BLOCK_M")))
-    tiles = (("m64n64", 64, 64, 32), ("m128n128", 128, 128, 16))
+    tiles = (("m64n64", 64, 64, 32), ("m128n128", 128, 128, 32))
     dims = (
         arg("m", "i32", "input_dim", index=0, axis=0),
         arg("n", "i32", "input_dim", index=1, axis=1),

@@ -16,10 +16,20 @@
 //   depth   d = (input channel, kernel row, kernel column)   (C*R*S)
 //   A[m][d] = W[m][c][r][s]  (OIHW is already row-major [K_out, C*R*S])
 //   B[d][j] = X[n][c][oh*sh - ph + r*dh][ow*sw - pw + s*dw]   (zero padded)
-// Workgroup = 4 wavefronts in a 2x2 grid; each wavefront owns a
-// (BM/2) x (BN/2) accumulator block made of 32x32 MFMA tiles. Operand tiles
-// are staged through LDS in depth-major order ([d][m] and [d][j]), double
-// buffered, with the next tile's global loads in flight during the MFMAs.
+//
+// Tiling. A workgroup (4 wavefronts) computes a BM x BN output tile and
+// walks the depth in BK-deep tiles, double buffered in LDS with the next
+// tile's global loads in flight during the MFMAs. The wavefronts form a
+// WGM x WGN x WGK grid: each owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA
+// accumulators over 1/WGK of every depth tile; WGK > 1 partial sums are added
+// through LDS before the epilogue.
+//
+// LDS holds both operands depth-contiguous, A as [m][d] and B as [j][d]
+// (rows padded by 4 floats), so one 16-byte read gives a lane four depths.
+// Within a depth tile the MFMA steps take the depths in the order
+//   step 4g + e, lane half h  ->  depth 8g + 4h + e
+// which visits every depth once; the sum is the same set of products.
+
 #include "common.h"
 
 namespace {
@@ -29,7 +39,7 @@ using ct::f32x4;
 
 enum Epilogue : int {
   kPlain = 0,             // y = acc
-  kBatchNorm = 1,         // y = (acc - mean) * rsqrt(var + eps) * scale + bias
+  kBatchNorm = 1,         // y = (acc - mean) * rsqrt(var + eps) * scale + bias, as one FMA
   kBatchNormRelu = 2,     // max(BN, 0)
   kBatchNormAddRelu = 3,  // max(BN + residual, 0)
   kColumnBias = 4,        // y = acc + bias[column]   (Gemm with a bias vector)
@@ -42,31 +52,70 @@ struct ConvGeometry {
 
 constexpr int kThreads = 256;
 
-template <int BM, int BN, int BK, int EPI>
-__device__ __forceinline__ void ConvCore(const float* __restrict__ x, const float* __restrict__ weight,
-                                         const float* __restrict__ scale, const float* __restrict__ bias,
-                                         const float* __restrict__ mean, const float* __restrict__ variance,
-                                         const float* __restrict__ residual, float* __restrict__ output,
-                                         const ConvGeometry g, const float epsilon) {
-  // Vector weight loads need every weight row to start 16-byte aligned.
-  const bool vec_a = ((g.c * g.r * g.s) & 3) == 0;
-  constexpr int WM = BM / 2;
-  constexpr int WN = BN / 2;
+// Raw buffer loads: an offset at or beyond the resource's byte range reads 0,
+// which is how zero padding and ragged tile edges are produced without
+// per-element branches. kNoRead is such an offset for every resource here
+// (tensors stay below 2 GiB).
+constexpr int kBufferFlags = 0x00020000;  // gfx9-family raw 32-bit buffer
+constexpr int kNoRead = 0x80000000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t Resource(const float* base, long long elements) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(elements * 4),
+                                           kBufferFlags);
+}
+
+__device__ __forceinline__ float LoadF32(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 0));
+}
+
+__device__ __forceinline__ f32x4 LoadF32x4(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
+// LDS layout of one ConvCore instantiation (in floats).
+template <int BM, int BN, int BK, int WGM, int WGN, int WGK>
+struct ConvLds {
+  static constexpr int kRow = BK + 4;                      // padded depth row
+  static constexpr int kA = BM * kRow;                     // one A buffer
+  static constexpr int kB = BN * kRow;                     // one B buffer
+  static constexpr int kTiles = 2 * (kA + kB);
+  static constexpr int kAccRegs = (BM / WGM / 32) * (BN / WGN / 32) * 16;
+  static constexpr int kReduce = (WGK - 1) * WGM * WGN * kAccRegs * 64;
+  static constexpr int kEpi = 2 * BM;
+  static constexpr int kFloats = (kTiles > kReduce ? kTiles : kReduce) + kEpi;
+};
+
+// POINTWISE: 1x1 kernel without padding, so every gathered pixel is inside
+// the image and a depth row is one input channel.
+template <int BM, int BN, int BK, int WGM, int WGN, int WGK, int EPI, bool POINTWISE>
+__device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* __restrict__ x,
+                                         const float* __restrict__ weight, const float* __restrict__ scale,
+                                         const float* __restrict__ bias, const float* __restrict__ mean,
+                                         const float* __restrict__ variance, const float* __restrict__ residual,
+                                         float* __restrict__ output, const ConvGeometry g, const float epsilon) {
+  using L = ConvLds<BM, BN, BK, WGM, WGN, WGK>;
+  constexpr int WM = BM / WGM;
+  constexpr int WN = BN / WGN;
   constexpr int TM = WM / 32;
   constexpr int TN = WN / 32;
-  constexpr int A_PER = BM * BK / kThreads;  // A elements per thread per tile
-  constexpr int B_PER = BK * BN / kThreads;  // B elements per thread per tile
-  constexpr int A_STRIDE = BM + 4;           // padded row of the [d][m] tile
-  static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
-  static_assert(kThreads % BN == 0, "B columns must divide the workgroup");
-  static_assert(A_PER % 4 == 0, "vector A loads need 4-element runs");
+  constexpr int ROW = L::kRow;
+  constexpr int GROUPS = BK / 8;                 // 8-depth groups per tile
+  constexpr int WAVE_GROUPS = GROUPS / WGK;      // groups per wavefront
+  constexpr int A_CHUNKS = BM * BK / 4 / kThreads;  // float4 chunks per thread
+  constexpr int B_RUN = BK * BN / kThreads;         // depths per thread (one column)
+  static_assert(WGM * WGN * WGK == kThreads / 64, "four wavefronts per workgroup");
+  static_assert(TM >= 1 && TN >= 1 && WAVE_GROUPS >= 1, "wave tile too small");
+  static_assert(A_CHUNKS >= 1 && A_CHUNKS * kThreads * 4 == BM * BK, "A tile split");
+  static_assert(kThreads % BN == 0 && B_RUN % 4 == 0, "B tile split");
 
-  __shared__ float a_tile[2][BK][A_STRIDE];
-  __shared__ float b_tile[2][BK][BN];
-  __shared__ float epi_mean[BM];
-  __shared__ float epi_rstd[BM];
-  __shared__ float epi_scale[BM];
-  __shared__ float epi_bias[BM];
+  float* a_tile = smem;                  // [2][BM][ROW]
+  float* b_tile = smem + 2 * L::kA;      // [2][BN][ROW]
+  constexpr int EPI_BASE = L::kTiles > L::kReduce ? L::kTiles : L::kReduce;
+  // BatchNorm folded per output channel: y = acc * epi_mul + epi_add with
+  // epi_mul = scale * rsqrt(var + eps), epi_add = bias - mean * epi_mul.
+  float* epi_mul = smem + EPI_BASE;
+  float* epi_add = epi_mul + BM;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -76,180 +125,232 @@ __device__ __forceinline__ void ConvCore(const float* __restrict__ x, const floa
   const int rs = g.r * g.s;
   const int depth = g.c * rs;
   const int columns = g.n * pq;
+  // Vector weight loads need every weight row to start 16-byte aligned.
+  const bool vec_a = (depth & 3) == 0;
 
   const int tiles_n = (columns + BN - 1) / BN;
   const int tiles_m = (g.k + BM - 1) / BM;
-  const int tile = ct::XcdContiguousIndex(blockIdx.x + blockIdx.y * gridDim.x, tiles_n * tiles_m);
-  const int m0 = (tile % tiles_m) * BM;
-  const int n0 = (tile / tiles_m) * BN;
+  const int tiles = tiles_n * tiles_m;
+  const int depth_tiles = (depth + BK - 1) / BK;
 
-  if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
-    for (int i = tid; i < BM; i += kThreads) {
-      const int m = m0 + i;
-      const bool ok = m < g.k;
-      epi_mean[i] = ok ? mean[m] : 0.0f;
-      epi_rstd[i] = ok ? rsqrtf(variance[m] + epsilon) : 0.0f;
-      epi_scale[i] = ok ? scale[m] : 0.0f;
-      epi_bias[i] = ok ? bias[m] : 0.0f;
-    }
-  }
-
-  // ---- B (im2col) loader state: one fixed column per thread.
+  // ---- B (im2col) loader: one fixed column per thread, a run of B_RUN
+  // consecutive depths. The run start is wave-uniform, so the (channel,
+  // kernel row, kernel column) walk stays in scalar registers.
   const int b_col = tid % BN;
-  const int b_row0 = (tid / BN) * B_PER;
-  const int j = n0 + b_col;
-  const bool col_ok = j < columns;
-  const int img = col_ok ? j / pq : 0;
-  const int pix = col_ok ? j - img * pq : 0;
-  const int oh = pix / g.q;
-  const int ow = pix - oh * g.q;
-  const int ih0 = oh * g.stride_h - g.pad_h;
-  const int iw0 = ow * g.stride_w - g.pad_w;
-  const float* x_img = x + static_cast<size_t>(img) * g.c * hw;
+  const int b_run0 = __builtin_amdgcn_readfirstlane(tid / BN) * B_RUN;
+  const __amdgpu_buffer_rsrc_t x_res = Resource(x, static_cast<long long>(g.n) * g.c * hw);
+  const __amdgpu_buffer_rsrc_t w_res = Resource(weight, static_cast<long long>(g.k) * depth);
+  int m0 = 0, n0 = 0;
+  bool col_ok = false;
+  int ih0 = 0, iw0 = 0;
+  // Element offset of (image, channel 0, ih0, iw0) and of the pointwise
+  // gather position; columns past the end read nothing.
+  int lane_base = 0, pw_base = 0;
 
-  float ra[A_PER];
-  float rb[B_PER];
+  // Selects output tile `t` (m-fastest order) and loads its per-channel
+  // epilogue parameters into LDS (visible after the next barrier).
+  auto setup_tile = [&](int t) {
+    m0 = (t % tiles_m) * BM;
+    n0 = (t / tiles_m) * BN;
+    if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
+      for (int i = tid; i < BM; i += kThreads) {
+        const int m = m0 + i;
+        const bool ok = m < g.k;
+        const float mul = ok ? scale[m] * rsqrtf(variance[m] + epsilon) : 0.0f;
+        epi_mul[i] = mul;
+        epi_add[i] = ok ? bias[m] - mean[m] * mul : 0.0f;
+      }
+    }
+    const int j = n0 + b_col;
+    col_ok = j < columns;
+    const int img = col_ok ? j / pq : 0;
+    const int pix = col_ok ? j - img * pq : 0;
+    const int oh = pix / g.q;
+    const int ow = pix - oh * g.q;
+    ih0 = oh * g.stride_h - g.pad_h;
+    iw0 = ow * g.stride_w - g.pad_w;
+    lane_base = img * g.c * hw + ih0 * g.w + iw0;
+    pw_base = img * g.c * hw + (oh * g.stride_h) * g.w + ow * g.stride_w;
+  };
+
+  f32x4 ra[A_CHUNKS];
+  float rb[B_RUN];
 
   auto load_tile = [&](int d0) {
-    // A: weights [K_out][depth], row-major.
-    if (vec_a) {
 #pragma unroll
-      for (int v = 0; v < A_PER / 4; ++v) {
-        const int f = tid + kThreads * v;
-        const int kq = f % (BK / 4);
-        const int m = f / (BK / 4);
-        const int d = d0 + kq * 4;
-        f32x4 val = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (m0 + m < g.k && d < depth) {
-          val = *reinterpret_cast<const f32x4*>(weight + static_cast<size_t>(m0 + m) * depth + d);
-        }
-        ra[v * 4 + 0] = val[0];
-        ra[v * 4 + 1] = val[1];
-        ra[v * 4 + 2] = val[2];
-        ra[v * 4 + 3] = val[3];
-      }
-    } else {
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int m = m0 + chunk / (BK / 4);
+      const int d = d0 + (chunk % (BK / 4)) * 4;
+      const int base = m * depth + d;
+      if (vec_a) {
+        ra[i] = LoadF32x4(w_res, (m < g.k && d < depth) ? base * 4 : kNoRead);
+      } else {
 #pragma unroll
-      for (int e = 0; e < A_PER; ++e) {
-        const int f = tid + kThreads * e;
-        const int kk = f % BK;
-        const int m = f / BK;
-        const int d = d0 + kk;
-        ra[e] = (m0 + m < g.k && d < depth) ? weight[static_cast<size_t>(m0 + m) * depth + d] : 0.0f;
+        for (int e = 0; e < 4; ++e) ra[i][e] = LoadF32(w_res, (m < g.k && d + e < depth) ? (base + e) * 4 : kNoRead);
       }
     }
-    // B: gathered input pixels, zero outside the image and past the depth.
-    int d = d0 + b_row0;
-    int ci = d / rs;
-    int rr = d - ci * rs;
-    int kr = rr / g.s;
-    int ks = rr - kr * g.s;
+    const int d = d0 + b_run0;  // wave-uniform
+    if (POINTWISE) {
 #pragma unroll
-    for (int e = 0; e < B_PER; ++e) {
-      const int ih = ih0 + kr * g.dil_h;
-      const int iw = iw0 + ks * g.dil_w;
-      const bool inside = col_ok && (d + e) < depth && static_cast<unsigned>(ih) < static_cast<unsigned>(g.h) &&
-                          static_cast<unsigned>(iw) < static_cast<unsigned>(g.w);
-      rb[e] = inside ? x_img[static_cast<size_t>(ci) * hw + ih * g.w + iw] : 0.0f;
-      if (++ks == g.s) {
-        ks = 0;
-        if (++kr == g.r) {
-          kr = 0;
-          ++ci;
+      for (int e = 0; e < B_RUN; ++e) {
+        rb[e] = LoadF32(x_res, (col_ok && d + e < depth) ? (pw_base + (d + e) * hw) * 4 : kNoRead);
+      }
+    } else {
+      int ci = d / rs;
+      const int rr = d - ci * rs;
+      int kr = rr / g.s;
+      int ks = rr - kr * g.s;
+#pragma unroll
+      for (int e = 0; e < B_RUN; ++e) {
+        const int dh = kr * g.dil_h;
+        const int dw = ks * g.dil_w;
+        const bool inside = col_ok && (d + e) < depth &&
+                            static_cast<unsigned>(ih0 + dh) < static_cast<unsigned>(g.h) &&
+                            static_cast<unsigned>(iw0 + dw) < static_cast<unsigned>(g.w);
+        rb[e] = LoadF32(x_res, inside ? (lane_base + ci * hw + dh * g.w + dw) * 4 : kNoRead);
+        if (++ks == g.s) {
+          ks = 0;
+          if (++kr == g.r) {
+            kr = 0;
+            ++ci;
+          }
         }
       }
     }
   };
 
   auto store_tile = [&](int buf) {
-    if (vec_a) {
+    float* at = a_tile + buf * L::kA;
+    float* bt = b_tile + buf * L::kB;
 #pragma unroll
-      for (int v = 0; v < A_PER / 4; ++v) {
-        const int f = tid + kThreads * v;
-        const int kq = f % (BK / 4);
-        const int m = f / (BK / 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a_tile[buf][kq * 4 + e][m] = ra[v * 4 + e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < A_PER; ++e) {
-        const int f = tid + kThreads * e;
-        a_tile[buf][f % BK][f / BK] = ra[e];
-      }
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int chunk = tid + kThreads * i;
+      *reinterpret_cast<f32x4*>(at + (chunk / (BK / 4)) * ROW + (chunk % (BK / 4)) * 4) = ra[i];
     }
 #pragma unroll
-    for (int e = 0; e < B_PER; ++e) b_tile[buf][b_row0 + e][b_col] = rb[e];
+    for (int e = 0; e < B_RUN; e += 4) {
+      const f32x4 v = {rb[e], rb[e + 1], rb[e + 2], rb[e + 3]};
+      *reinterpret_cast<f32x4*>(bt + b_col * ROW + b_run0 + e) = v;
+    }
   };
 
   f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int t = 0; t < TN; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][t][r] = 0.0f;
 
-  const int wm = (wave >> 1) * WM;
-  const int wn = (wave & 1) * WN;
-  const int half = lane >> 5;  // which depth row of the MFMA k-pair
+  const int wk = wave / (WGM * WGN);
+  const int wmn = wave % (WGM * WGN);
+  const int wm = (wmn / WGN) * WM;
+  const int wn = (wmn % WGN) * WN;
+  const int half = lane >> 5;
   const int lane32 = lane & 31;
-  const int depth_tiles = (depth + BK - 1) / BK;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  // Accumulates depth tiles [kb, ke) of the current output tile into acc.
+  // Ends with a barrier, after which the LDS tiles are free.
+  auto run_depth = [&](int kb, int ke) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][t][r] = 0.0f;
+    load_tile(kb * BK);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = kb; kt < ke; ++kt) {
+      const int cur = (kt - kb) & 1;
+      const bool more = kt + 1 < ke;
+      if (more) load_tile((kt + 1) * BK);
+      const float* at = a_tile + cur * L::kA + (wm + lane32) * ROW + 4 * half;
+      const float* bt = b_tile + cur * L::kB + (wn + lane32) * ROW + 4 * half;
+#pragma unroll
+      for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
+        const int col = (wk * WAVE_GROUPS + gi) * 8;
+        f32x4 av[TM];
+        f32x4 bv[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const f32x4*>(at + i * 32 * ROW + col);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) bv[t] = *reinterpret_cast<const f32x4*>(bt + t * 32 * ROW + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int t = 0; t < TN; ++t)
+              acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[t][e], acc[i][t], 0, 0, 0);
+      }
+      if (more) store_tile(cur ^ 1);
+      __syncthreads();
+    }
+  };
 
-  for (int kt = 0; kt < depth_tiles; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < depth_tiles;
-    if (more) load_tile((kt + 1) * BK);
+  // Epilogue of the current tile. Lane holds column (lane % 32) of each
+  // 32x32 tile and rows 8*(r/4) + 4*(lane/32) + (r%4) for register r.
+  auto from_acc = [&](int i, int t, int r) { return acc[i][t][r]; };
+  auto store_output = [&](auto value) {
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      float av[TM];
-      float bv[TN];
+    for (int t = 0; t < TN; ++t) {
+      const int col = n0 + wn + t * 32 + lane32;
+      if (col >= columns) continue;
+      const int cimg = col / pq;
+      const int cpix = col - cimg * pq;
+      const size_t col_base = static_cast<size_t>(cimg) * g.k * pq + cpix;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) av[i] = a_tile[cur][kk + half][wm + i * 32 + lane32];
+      for (int i = 0; i < TM; ++i) {
 #pragma unroll
-      for (int t = 0; t < TN; ++t) bv[t] = b_tile[cur][kk + half][wn + t * 32 + lane32];
+        for (int r = 0; r < 16; ++r) {
+          const int lrow = wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int row = m0 + lrow;
+          if (row >= g.k) continue;
+          float v = value(i, t, r);
+          const size_t at = col_base + static_cast<size_t>(row) * pq;
+          if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
+            // Rows r..r+3 of a group are consecutive channels: one 16-byte read.
+            const f32x4 mul = *reinterpret_cast<const f32x4*>(epi_mul + (lrow & ~3));
+            const f32x4 add = *reinterpret_cast<const f32x4*>(epi_add + (lrow & ~3));
+            v = fmaf(v, mul[r & 3], add[r & 3]);
+          }
+          if (EPI == kBatchNormAddRelu) v += residual[at];
+          if (EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v = fmaxf(v, 0.0f);
+          if (EPI == kColumnBias) v += bias[col];
+          output[at] = v;
+        }
+      }
+    }
+  };
+
+  setup_tile(ct::XcdContiguousIndex(blockIdx.x + blockIdx.y * gridDim.x, tiles));
+  run_depth(0, depth_tiles);
+
+  // ---- Depth-split partial sums: wavefronts wk > 0 add theirs to wk == 0
+  // through LDS (register r of lane l lands at [slot][r][l]).
+  if (WGK > 1) {
+    constexpr int REGS = TM * TN * 16;
+    float* red = smem;
+    if (wk > 0) {
+      float* mine = red + ((wk - 1) * WGM * WGN + wmn) * REGS * 64;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[t], acc[i][t], 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mine[((i * TN + t) * 16 + r) * 64 + lane] = acc[i][t][r];
     }
-    if (more) store_tile(cur ^ 1);
     __syncthreads();
+    if (wk > 0) return;
+#pragma unroll 1
+    for (int s = 1; s < WGK; ++s) {
+      const float* theirs = red + ((s - 1) * WGM * WGN + wmn) * REGS * 64;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][t][r] += theirs[((i * TN + t) * 16 + r) * 64 + lane];
+    }
   }
 
-  // ---- Epilogue. Lane holds column (lane % 32) of each 32x32 tile and rows
-  // 8*(r/4) + 4*(lane/32) + (r%4) for accumulator register r.
-#pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int col = n0 + wn + t * 32 + lane32;
-    if (col >= columns) continue;
-    const int cimg = col / pq;
-    const int cpix = col - cimg * pq;
-    const size_t col_base = static_cast<size_t>(cimg) * g.k * pq + cpix;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lrow = wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        const int row = m0 + lrow;
-        if (row >= g.k) continue;
-        float v = acc[i][t][r];
-        const size_t at = col_base + static_cast<size_t>(row) * pq;
-        if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
-          v = (v - epi_mean[lrow]) * epi_rstd[lrow] * epi_scale[lrow] + epi_bias[lrow];
-        }
-        if (EPI == kBatchNormAddRelu) v += residual[at];
-        if (EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v = fmaxf(v, 0.0f);
-        if (EPI == kColumnBias) v += bias[col];
-        output[at] = v;
-      }
-    }
-  }
+  store_output(from_acc);
 }
 
 __device__ __forceinline__ ConvGeometry MakeGeometry(int n, int c, int h, int w, int k, int r, int s, int out_h,
@@ -270,53 +371,66 @@ __device__ __forceinline__ ConvGeometry MakeGeometry(int n, int c, int h, int w,
 #define CT_CONV_GEOMETRY \
   MakeGeometry(n, c, h, w, k, r, s, out_h, out_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w)
 
-#define CT_DISPATCH_A(BM, BN, BK, EPI, ...) ConvCore<BM, BN, BK, EPI>(__VA_ARGS__);
+// One LDS buffer per kernel, shared by the pointwise and general paths.
+#define CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, EPI, ...)                                             \
+  __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];  \
+  if (r == 1 && s == 1 && pad_h == 0 && pad_w == 0) {                                               \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, true>(smem, __VA_ARGS__);                              \
+  } else {                                                                                          \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, false>(smem, __VA_ARGS__);                             \
+  }
 
-#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK)                                                        \
+#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                          \
   CT_KERNEL void __launch_bounds__(kThreads) conv_bn_relu_fp32_##NAME(                                  \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
-    CT_DISPATCH_A(BM, BN, BK, kBatchNormRelu, x, weight, scale, bias, mean, variance, nullptr, output,  \
-                  CT_CONV_GEOMETRY, epsilon)                                                             \
+    CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormRelu, x, weight, scale, bias, mean, variance,      \
+                nullptr, output, CT_CONV_GEOMETRY, epsilon)                                              \
   }                                                                                                      \
   CT_KERNEL void __launch_bounds__(kThreads) conv_bn_fp32_##NAME(                                       \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
-    CT_DISPATCH_A(BM, BN, BK, kBatchNorm, x, weight, scale, bias, mean, variance, nullptr, output,      \
-                  CT_CONV_GEOMETRY, epsilon)                                                             \
+    CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNorm, x, weight, scale, bias, mean, variance, nullptr, \
+                output, CT_CONV_GEOMETRY, epsilon)                                                       \
   }                                                                                                      \
   CT_KERNEL void __launch_bounds__(kThreads) conv_bn_add_relu_fp32_##NAME(                              \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon, void*,   \
       void*) {                                                                                           \
-    CT_DISPATCH_A(BM, BN, BK, kBatchNormAddRelu, x, weight, scale, bias, mean, variance, residual,      \
-                  output, CT_CONV_GEOMETRY, epsilon)                                                     \
+    CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormAddRelu, x, weight, scale, bias, mean, variance,   \
+                residual, output, CT_CONV_GEOMETRY, epsilon)                                             \
   }                                                                                                      \
   CT_KERNEL void __launch_bounds__(kThreads) conv_fp32_##NAME(const float* x, const float* weight,      \
                                                               float* output, CT_CONV_DIMS, void*, void*) { \
-    CT_DISPATCH_A(BM, BN, BK, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr, nullptr, output,   \
-                  CT_CONV_GEOMETRY, 0.0f)                                                                \
+    CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr,       \
+                nullptr, output, CT_CONV_GEOMETRY, 0.0f)                                                 \
   }
 
-CT_DEFINE_CONV_VARIANTS(m128n128, 128, 128, 16)
-CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32)
-CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 16)
-CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32)
+// name, BM, BN, BK, WGM, WGN, WGK
+CT_DEFINE_CONV_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1)
+CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2)
+CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2)
+CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
-// depth-major core with rows = m, columns = n, depth = k (a 1x1 convolution
-// of one 1 x n "image").
-#define CT_DEFINE_GEMM_VARIANTS(NAME, BM, BN, BK)                                                         \
+// core with rows = m, columns = n, depth = k (a 1x1 convolution of one
+// 1 x n "image").
+#define CT_DEFINE_GEMM_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                           \
   CT_KERNEL void __launch_bounds__(kThreads) gemm_fp32_##NAME(const float* a, const float* b, float* output, \
                                                               int m, int n, int k, void*, void*) {        \
+    __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
-    ConvCore<BM, BN, BK, kPlain>(b, a, nullptr, nullptr, nullptr, nullptr, nullptr, output, g, 0.0f); \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, kPlain, true>(smem, b, a, nullptr, nullptr, nullptr, nullptr,     \
+                                                      nullptr, output, g, 0.0f);                          \
   }                                                                                                       \
   CT_KERNEL void __launch_bounds__(kThreads) gemm_bias_fp32_##NAME(                                      \
       const float* a, const float* b, const float* bias, float* output, int m, int n, int k, void*, void*) { \
+    __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
-    ConvCore<BM, BN, BK, kColumnBias>(b, a, nullptr, bias, nullptr, nullptr, nullptr, output, g, 0.0f); \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, kColumnBias, true>(smem, b, a, nullptr, bias, nullptr, nullptr,   \
+                                                           nullptr, output, g, 0.0f);                     \
   }
 
-CT_DEFINE_GEMM_VARIANTS(m64n64, 64, 64, 32)
-CT_DEFINE_GEMM_VARIANTS(m128n128, 128, 128, 16)
+CT_DEFINE_GEMM_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
+CT_DEFINE_GEMM_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)

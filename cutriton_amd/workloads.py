@@ -163,6 +163,33 @@ def ffn(tokens: int, hidden: int, intermediate: int, seed: int = SEED) -> tuple[
     return g, x
 
 
+def ffn_pattern(tokens: int = 17, hidden: int = 128, intermediate: int = 512) -> tuple[GraphSpec, dict[str, np.ndarray]]:
+    """FP16 Gemm -> Gelu -> Add(residual) -> LayerNormalization with the
+    integer-pattern inputs of the reference's transformer test
+    (tests/cpp/test_cuda.cpp:336-358, graph 300-333): x[t*H+i] = ((i%23)-11)/37,
+    residual ((i%17)-8)/53, W ((i%19)-9)/181, scale 0.9+0.001*(c%13),
+    bias ((c%7)-3)/100, epsilon 1e-5. Returns (graph, feeds)."""
+    f16 = np.float16
+    x = ((np.arange(tokens * hidden) % 23 - 11) / 37.0).astype(f16).reshape(tokens, hidden)
+    residual = ((np.arange(tokens * intermediate) % 17 - 8) / 53.0).astype(f16).reshape(tokens, intermediate)
+    w = ((np.arange(hidden * intermediate) % 19 - 9) / 181.0).astype(f16).reshape(hidden, intermediate)
+    c = np.arange(intermediate)
+    scale = (0.9 + 0.001 * (c % 13)).astype(f16)
+    bias = (((c % 7) - 3) / 100.0).astype(f16)
+    g = GraphSpec()
+    g.inputs["x"] = ((tokens, hidden), "float16", "")
+    g.inputs["residual"] = ((tokens, intermediate), "float16", "")
+    g.constant("weight", w)
+    g.constant("scale", scale)
+    g.constant("bias", bias)
+    g.add("projection", "Gemm", ["x", "weight"], ["projected"])
+    g.add("activation", "Gelu", ["projected"], ["activated"])
+    g.add("residual_add", "Add", ["activated", "residual"], ["sum"])
+    g.add("output_norm", "LayerNormalization", ["sum", "scale", "bias"], ["output"], axis=-1, epsilon=1e-5)
+    g.outputs.append("output")
+    return g, {"x": x, "residual": residual}
+
+
 def stem_kat(batch_shape: tuple[int, ...] = (1, 3, 224, 224)) -> tuple[GraphSpec, np.ndarray, np.ndarray]:
     """Known-answer stem: returns (graph, input, expected logits).
 

@@ -41,12 +41,17 @@ struct LoweringContext {
 };
 
 // Valid only for the duration of OpKernel::Compute. `stream` is a
-// hipStream_t for the HIP backend.
+// hipStream_t for the HIP backend. `runtime_scratch` is the execution
+// context's zero-initialised device scratch (runtime_scratch_bytes long),
+// bound to the first runtime_reserved argument of kernels that declare a
+// scratch size; such kernels leave it zeroed again when they finish.
 struct KernelContext {
   const Node* node{nullptr};
   std::unordered_map<std::string, Tensor>* tensors{nullptr};
   void* stream{nullptr};
   Profiler* profiler{nullptr};
+  void* runtime_scratch{nullptr};
+  std::size_t runtime_scratch_bytes{0};
 };
 
 class OpKernel {

@@ -111,6 +111,9 @@ struct KernelArtifact {
   int num_warps{4};
   int num_stages{1};
   int shared_memory_bytes{0};
+  // Device scratch the kernel needs through its first runtime_reserved
+  // argument (0: the argument is null, as in the reference ABI).
+  std::int64_t runtime_scratch_bytes{0};
   std::array<GridExpression, 3> launch_grid{};
   std::unordered_map<std::string, int64_t> launch_meta;
   // ABI v1 compatibility: grid = ceil(output_numel / grid_divisor).

@@ -55,6 +55,12 @@ class ExecutionContext {
   const std::unordered_map<std::string, Tensor>& tensors() const { return tensors_; }
   // Index of the chosen candidate per plan op (valid after the first run).
   const std::vector<std::size_t>& selected_candidates() const { return selected_candidates_; }
+  // Kernel time of plan op `op_index` as selected: one warm-up launch, then
+  // `iterations` back-to-back launches between one hipEvent pair on `stream`
+  // (the context's own stream when null), so that launch latency overlaps
+  // execution. Needs a completed run; the op reads and rewrites its bound
+  // tensors. Ops without a kernel (Flatten views) report 0.
+  Status TimeOp(std::size_t op_index, int iterations, void* stream, double* ms_per_launch);
 
  private:
   Status PrepareKernels();
@@ -80,6 +86,10 @@ class ExecutionContext {
   std::vector<std::vector<std::unique_ptr<OpKernel>>> kernels_;
   std::unordered_map<std::string, Tensor> tensors_;
   std::shared_ptr<Buffer> workspace_;
+  // Zero-initialised device scratch for kernels that declare one.
+  std::shared_ptr<Buffer> runtime_scratch_;
+  void* ScratchPointer() const { return runtime_scratch_ ? runtime_scratch_->data() : nullptr; }
+  std::size_t ScratchBytes() const { return runtime_scratch_ ? runtime_scratch_->size_bytes() : 0; }
   Profiler profiler_;
   // HIP stream/event/graph state; its type lives in the implementation.
   void* hip_state_{nullptr};

@@ -124,6 +124,10 @@ int ct_context_profile_event(const ct_context* context, int index, char* name,
 size_t ct_context_graph_count(const ct_context* context);
 size_t ct_context_module_count(const ct_context* context);
 int ct_context_selected_candidate(const ct_context* context, int op_index);
+/* Kernel time per launch of plan op `op_index` (ExecutionContext::TimeOp):
+ * `iterations` back-to-back launches between one event pair on `stream`. */
+int ct_context_time_op(ct_context* context, int op_index, int iterations, void* stream,
+                       double* ms_per_launch);
 
 #ifdef __cplusplus
 }

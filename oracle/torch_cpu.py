@@ -22,8 +22,9 @@ def _pads(attrs: Mapping[str, Any]) -> list[int]:
     return list(attrs.get("pads", [0, 0, 0, 0]))
 
 
-def prepare(graph: Any) -> dict[str, torch.Tensor]:
-    return {name: torch.from_numpy(np.ascontiguousarray(arr, dtype=np.float32))
+def prepare(graph: Any, dtype: torch.dtype = torch.float32) -> dict[str, torch.Tensor]:
+    np_dtype = np.float64 if dtype == torch.float64 else np.float32
+    return {name: torch.from_numpy(np.ascontiguousarray(arr, dtype=np_dtype))
             for name, (arr, _) in graph.constants.items()}
 
 

@@ -64,6 +64,16 @@ def only_variant(kernel_id: str, variant_id: str):
     return keep
 
 
+def only_kernel_variant(kernel_id: str, variant_id: str, family_prefix: str):
+    """Keeps only `variant_id` of `kernel_id` among the kernels whose id starts
+    with `family_prefix` (the sibling implementations of the same op)."""
+    def keep(e: dict) -> bool:
+        if not e["kernel_id"].startswith(family_prefix + "."):
+            return True
+        return e["kernel_id"] == kernel_id and e["variant_id"] == variant_id
+    return keep
+
+
 def without_kernels(kernel_ids: Iterable[str]):
     ids = set(kernel_ids)
     return lambda e: e["kernel_id"] not in ids

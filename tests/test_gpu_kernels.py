@@ -14,11 +14,13 @@ import pytest
 
 from cutriton_amd import engine, workloads
 from oracle import oracle
-from tests.helpers import assert_close_fp32, filtered_pack, only_variant, run_graph, without_kernels
+from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant, only_variant, run_graph,
+                           without_kernels)
 
 pytestmark = pytest.mark.gpu
 
-CONV_VARIANTS = ("m128n128", "m64n128", "m128n64", "m64n64")
+CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
+                 "direct:d64n256", "direct:d64n64", "direct:d32n64")
 GEMM16_VARIANTS = ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64")
 
 
@@ -62,16 +64,18 @@ CONV_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("variant", CONV_VARIANTS)
-@pytest.mark.parametrize("tail,kernel_id", [
-    ("relu", "conv_bn_relu.fp32.nchw.mfma"),
-    ("bn", "conv_bn.fp32.nchw.mfma"),
-    ("add_relu", "conv_bn_add_relu.fp32.nchw.mfma"),
-    ("conv", "conv.fp32.nchw.mfma"),
+@pytest.mark.parametrize("family_variant", CONV_VARIANTS)
+@pytest.mark.parametrize("tail,kernel_base", [
+    ("relu", "conv_bn_relu.fp32.nchw"),
+    ("bn", "conv_bn.fp32.nchw"),
+    ("add_relu", "conv_bn_add_relu.fp32.nchw"),
+    ("conv", "conv.fp32.nchw"),
 ])
-def test_conv_family_variants(tmp_path, variant, tail, kernel_id):
+def test_conv_family_variants(tmp_path, family_variant, tail, kernel_base):
     rng = np.random.default_rng(7)
-    pack = filtered_pack(tmp_path / "pack", only_variant(kernel_id, variant))
+    family, variant = family_variant.split(":")
+    kernel_id = f"{kernel_base}.{family}"
+    pack = filtered_pack(tmp_path / "pack", only_kernel_variant(kernel_id, variant, kernel_base))
     for shape in CONV_SHAPES:
         g, feeds = conv_graph(rng, *shape, tail=tail)
         opts = engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled")

@@ -83,3 +83,41 @@ def test_ffn_config_m4096():
     out, _, _ = run_graph(g, {"x": x})
     err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, {"x": x})["y"])
     assert err.max() <= 1e-2, err.max()
+
+
+@pytest.mark.parametrize("tuning", ["disabled", "tune_on_miss"])
+def test_ffn_integer_pattern(tuning, tmp_path):
+    """The reference's FP16 transformer test inputs (tokens 17, hidden 128,
+    intermediate 512; tests/cpp/test_cuda.cpp:336-393): Gemm -> Gelu ->
+    Add(residual) -> LayerNormalization fuses to GemmGelu +
+    SkipLayerNormalization and matches the FP64 oracle within 1e-2."""
+    g, feeds = workloads.ffn_pattern()
+    opts = engine.CompileOptions(tuning_mode=tuning, tuning_cache_dir=str(tmp_path), enable_profiling=True)
+    out, eng, ctx = run_graph(g, feeds, opts, repeats=2)
+    assert [op.op_type for op in eng.ops()] == ["GemmGelu", "SkipLayerNormalization"]
+    err = np.abs(out["output"].astype(np.float64) - oracle.evaluate(g, feeds)["output"])
+    assert err.max() <= 1e-2, err.max()
+    assert len(ctx.profile_events()) == 2
+
+
+def test_time_op_reports_kernel_time():
+    """ExecutionContext::TimeOp: positive per-launch kernel time for ops with
+    kernels, 0 for the Flatten view, an error before the first run."""
+    g, x, _ = workloads.stem_kat()
+    eng = engine.build_engine(workloads.to_model(g), engine.CompileOptions(tuning_mode="disabled"))
+    ctx = eng.create_execution_context()
+    import torch
+
+    xi = torch.from_numpy(x).to("cuda:0")
+    shape, _ = eng.value_desc("output")
+    y = torch.empty(shape, device="cuda:0")
+    ctx.bind_input("input", xi)
+    ctx.bind_output("output", y)
+    with pytest.raises(engine.CutritonError):
+        ctx.time_op(0, 5)
+    ctx.run()
+    before = y.cpu().numpy().copy()
+    times = [ctx.time_op(i, 5) for i in range(len(eng.ops()))]
+    assert times[0] > 0 and times[2] == 0.0 and times[3] > 0
+    ctx.run()
+    assert np.array_equal(before, y.cpu().numpy())
