@@ -78,5 +78,13 @@ def library() -> ctypes.CDLL:
             raise RuntimeError(f"{LIBRARY_PATH} is missing: run __graft_entry__.build() first")
         if not (PACK_DIR / "pack.json").exists():
             raise RuntimeError(f"{PACK_DIR / 'pack.json'} is missing: run __graft_entry__.build() first")
+        # torch ships its own libamdhip64 under the soname this library needs
+        # (libamdhip64.so.7). One process must hold one HIP runtime: load
+        # torch's first when torch is installed, so that both bind to it.
+        # Loaded the other way round, torch's device initialisation fails.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         _LIBRARY = ctypes.CDLL(str(LIBRARY_PATH))
     return _LIBRARY

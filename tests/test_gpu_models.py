@@ -121,3 +121,64 @@ def test_time_op_reports_kernel_time():
     assert times[0] > 0 and times[2] == 0.0 and times[3] > 0
     ctx.run()
     assert np.array_equal(before, y.cpu().numpy())
+
+
+def _profile_context(graph, opts):
+    eng = engine.build_engine(workloads.to_model(graph), opts)
+    return eng, eng.create_execution_context()
+
+
+def _run_shape(ctx, eng, feeds: dict[str, np.ndarray], out_name: str, layout: str):
+    import torch
+
+    for name, value in feeds.items():
+        ctx.set_input_shape(name, value.shape)
+    ctx.resolve_shapes()
+    keep = []
+    for name, value in feeds.items():
+        t = torch.from_numpy(np.ascontiguousarray(value)).to("cuda:0")
+        keep.append(t)
+        ctx.bind_input(name, t, layout=layout)
+    shape, dtype, _ = ctx.resolved_desc(out_name)
+    out = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
+    ctx.bind_output(out_name, out, layout="")
+    ctx.run()
+    ctx.run()  # graph replay
+    return out.cpu().numpy()
+
+
+def test_resnet50_dynamic_batch_profile_32_and_64(tmp_path):
+    """Profile min1/opt32/max64, workspace planned at the profile max, run at
+    batch 32 then 64 on one context (a hipGraph per shape). Images are
+    checked against the FP64 oracle, one per batch end."""
+    g = workloads.resnet50(1)
+    opts = engine.CompileOptions(tuning_mode="tune_on_miss", tuning_cache_dir=str(tmp_path), shape_profiles={
+        "batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224), (64, 3, 224, 224))}})
+    eng, ctx = _profile_context(g, opts)
+    ctx.select_shape_profile("batch")
+    x64 = workloads.resnet50_input(64)
+    for batch in (32, 64):
+        out = _run_shape(ctx, eng, {"input": x64[:batch]}, "output", "NCHW")
+        assert out.shape == (batch, 1000)
+        for i in (0, batch - 1):
+            want = oracle.evaluate(g, {"input": x64[i:i + 1]})["output"]
+            check_logits(out[i:i + 1].astype(np.float64), want)
+    assert ctx.cached_hip_graph_count() == 2
+
+
+def test_ffn_dynamic_m_profile(tmp_path):
+    """FFN with the M profile min128/opt4096/max8192 and tuned variants, run
+    at M = 128, 4096 and 8192. Rows are independent (GEMM rows, per-row
+    LayerNorm), so the FP64 check evaluates the first and last 64 rows."""
+    g, x = workloads.ffn(8192, 1024, 4096)
+    opts = engine.CompileOptions(tuning_mode="tune_on_miss", tuning_cache_dir=str(tmp_path), shape_profiles={
+        "tokens": {"x": ((128, 1024), (4096, 1024), (8192, 1024))}})
+    eng, ctx = _profile_context(g, opts)
+    ctx.select_shape_profile("tokens")
+    for m in (128, 4096, 8192):
+        out = _run_shape(ctx, eng, {"x": x[:m]}, "y", "")
+        assert out.shape == (m, 1024)
+        for rows in (slice(0, 64), slice(m - 64, m)):
+            want = oracle.evaluate(g, {"x": x[rows]})["y"]
+            err = np.abs(out[rows].astype(np.float64) - want).max()
+            assert err <= 1e-2, (m, rows, err)
