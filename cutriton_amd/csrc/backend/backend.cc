@@ -60,6 +60,16 @@ Status CheckTensor(const Graph& graph, const std::string& name, const Device& de
   return Status::OK();
 }
 
+std::vector<std::string> InvocationInputs(const KernelArtifact& artifact, std::vector<std::string> inputs) {
+  for (const auto& argument : artifact.arguments) {
+    const KernelArgumentSource& s = argument.source;
+    if (s.layout.empty() || s.index < 0 || static_cast<std::size_t>(s.index) >= inputs.size()) continue;
+    std::string& name = inputs[static_cast<std::size_t>(s.index)];
+    name = LaidOutConstantName(name, s.layout);
+  }
+  return inputs;
+}
+
 std::string BaseArch(const std::string& full) {
   const auto colon = full.find(':');
   return colon == std::string::npos ? full : full.substr(0, colon);
@@ -80,6 +90,17 @@ bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const Val
   if (!node.inputs().empty() && !layout_ok(node.inputs().front())) return false;
   for (const auto& name : node.outputs()) {
     if (!layout_ok(name)) return false;
+  }
+  // An input read in another layout must be a rank-4 FP32 constant: the
+  // engine re-lays it out once, at constant upload.
+  for (const auto& argument : artifact.arguments) {
+    const KernelArgumentSource& s = argument.source;
+    if (s.layout.empty()) continue;
+    if (s.index < 0 || static_cast<std::size_t>(s.index) >= node.inputs().size()) return false;
+    const ValueDesc* v = lookup(node.inputs()[static_cast<std::size_t>(s.index)]);
+    if (v == nullptr || !v->is_constant || v->tensor.shape.size() != 4 || v->tensor.dtype != DataType::kFloat32) {
+      return false;
+    }
   }
   for (const auto& c : artifact.constraints) {
     switch (c.kind) {
@@ -185,7 +206,8 @@ class HipBackend final : public Backend {
       ExecutionCandidate candidate;
       candidate.candidate_id = artifact->identity();
       candidate.is_default = artifact->is_default;
-      candidate.steps.push_back(KernelInvocation{*artifact, node.inputs(), node.outputs()});
+      candidate.steps.push_back(
+          KernelInvocation{*artifact, InvocationInputs(*artifact, node.inputs()), node.outputs()});
       candidates->push_back(std::move(candidate));
     }
     CUTRITON_RETURN_IF_ERROR(RegisterBuiltinFusionAlternatives());
@@ -231,7 +253,8 @@ class HipBackend final : public Backend {
       for (const auto& artifact : *list) {
         if (artifact.is_default && artifact.dtype == dtype &&
             ArtifactMatches(artifact, probe, lookup, capability, arch)) {
-          candidate->steps.push_back(KernelInvocation{artifact, std::move(inputs), {std::move(output)}});
+          candidate->steps.push_back(
+              KernelInvocation{artifact, InvocationInputs(artifact, std::move(inputs)), {std::move(output)}});
           return true;
         }
       }

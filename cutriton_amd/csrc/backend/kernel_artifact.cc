@@ -138,6 +138,12 @@ KernelArgumentSpec ParseArgument(const Value& v) {
   s.attribute_index = IntOr(source, "index", 0);
   s.default_int = IntOr(source, "default", 0);
   s.default_float = DoubleOr(source, "default", 0.0);
+  if (const Value* layout = source.find("layout")) {
+    s.layout = layout->string();
+    if (s.kind != KernelArgumentSourceKind::kInput || s.layout != "OHWI") {
+      throw std::runtime_error("argument " + argument.name + ": only an input may request a layout, and only OHWI");
+    }
+  }
   return argument;
 }
 

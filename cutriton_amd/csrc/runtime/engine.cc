@@ -316,6 +316,61 @@ class EngineState {
       CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(bytes, value->tensor.ByteSize()));
       device_constants.emplace(entry.first, Tensor(value->tensor, std::move(buffer)));
     }
+    return UploadLaidOutConstants();
+  }
+
+  // Copies of constants in the layout a selected kernel reads them in (the
+  // KernelInvocation input "<constant>#<layout>"), made once per engine.
+  // The copy keeps the logical shape; only the element order changes.
+  Status UploadLaidOutConstants() {
+    const Device& device = plan.backend_options().device;
+    if (device.type != DeviceType::kHIP) return Status::OK();
+    for (const PlanOp& op : plan.ops()) {
+      for (const ExecutionCandidate& candidate : op.candidates) {
+        for (const PlanStep& step : candidate.steps) {
+          const auto* inv = std::get_if<KernelInvocation>(&step);
+          if (inv == nullptr) continue;
+          for (const auto& argument : inv->artifact.arguments) {
+            const KernelArgumentSource& src = argument.source;
+            if (src.layout.empty() || src.index < 0 || static_cast<std::size_t>(src.index) >= inv->inputs.size()) {
+              continue;
+            }
+            const std::string& name = inv->inputs[static_cast<std::size_t>(src.index)];
+            if (device_constants.count(name) != 0) continue;
+            const std::string base = name.substr(0, name.rfind('#'));
+            const auto host = plan.constants().find(base);
+            if (host == plan.constants().end() || src.layout != "OHWI") {
+              return Status::Internal("no constant to lay out as " + name);
+            }
+            const TensorDesc& desc = host->second.desc();
+            if (desc.shape.size() != 4 || desc.dtype != DataType::kFloat32) {
+              return Status::InvalidArgument("OHWI needs a rank-4 float32 constant: " + base);
+            }
+            const int64_t k = desc.shape[0], c = desc.shape[1], r = desc.shape[2], w = desc.shape[3];
+            TensorDesc laid_out = desc;
+            laid_out.layout = "OHWI";
+            if (r * w == 1) {  // [K][C][1][1]: both orders are the same bytes
+              device_constants.emplace(name, Tensor(laid_out, device_constants.at(base).buffer(),
+                                                    device_constants.at(base).byte_offset()));
+              continue;
+            }
+            const auto* in = reinterpret_cast<const float*>(static_cast<const std::uint8_t*>(host->second.buffer()->data()) +
+                                                            host->second.byte_offset());
+            std::vector<float> out(static_cast<std::size_t>(k * c * r * w));
+            for (int64_t o = 0; o < k; ++o)
+              for (int64_t i = 0; i < c; ++i)
+                for (int64_t y = 0; y < r; ++y)
+                  for (int64_t x = 0; x < w; ++x)
+                    out[static_cast<std::size_t>(((o * r + y) * w + x) * c + i)] =
+                        in[static_cast<std::size_t>(((o * c + i) * r + y) * w + x)];
+            std::shared_ptr<Buffer> buffer;
+            CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(desc.ByteSize(), device.id, &buffer));
+            CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(out.data(), desc.ByteSize()));
+            device_constants.emplace(name, Tensor(laid_out, std::move(buffer)));
+          }
+        }
+      }
+    }
     return Status::OK();
   }
 

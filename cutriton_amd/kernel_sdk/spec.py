@@ -20,8 +20,12 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Any
 
+# An input may ask for another layout of a constant of the same logical shape;
+# OHWI stores an OIHW convolution weight as [out][kh][kw][in].
+INPUT_LAYOUTS = frozenset({"OHWI"})
+
 ARGUMENT_SOURCES: dict[str, frozenset[str]] = {
-    "input": frozenset({"kind", "index"}),
+    "input": frozenset({"kind", "index", "layout"}),
     "output": frozenset({"kind", "index"}),
     "input_dim": frozenset({"kind", "index", "axis"}),
     "input_dim_product": frozenset({"kind", "index", "begin_axis"}),
@@ -124,6 +128,8 @@ class KernelSpec:
                 )
             if argument.type not in ARGUMENT_TYPES:
                 raise ValueError(f"{self.kernel_id}: unsupported argument type {argument.type}")
+            if "layout" in argument.source and argument.source["layout"] not in INPUT_LAYOUTS:
+                raise ValueError(f"{self.kernel_id}: unknown input layout for {argument.name}")
         reserved = [i for i, a in enumerate(self.arguments) if a.source.get("kind") == "runtime_reserved"]
         if reserved != [len(self.arguments) - 2, len(self.arguments) - 1]:
             raise ValueError(f"{self.kernel_id}: the ABI requires two trailing runtime_reserved arguments")

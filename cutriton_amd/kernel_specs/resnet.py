@@ -75,6 +75,29 @@ def conv_variants(prefix: str) -> tuple[KernelVariant, ...]:
     )
 
 
+# Split-K variants (conv_fp32.hip): (variant id, BLOCK_M, BLOCK_N, BLOCK_K, SPLIT). SPLIT
+# workgroups share one output tile's depth; they need runtime scratch for the
+# per-tile counters (16384 x 4 bytes) and the partial sums (128 MiB).
+SPLIT_TILES = (
+    ("m128n128s2", 128, 128, 32, 2),
+    ("m128n128s4", 128, 128, 32, 4),
+    ("m128n128s8", 128, 128, 32, 8),
+)
+SPLIT_DEFAULT = "m128n128s4"
+SPLIT_SCRATCH_BYTES = 16384 * 4 + (128 << 20)
+# x: ceil(N*P*Q / BLOCK_N), y: ceil(K_out / BLOCK_M), z: SPLIT.
+SPLIT_GRID = CONV_GRID + (meta("SPLIT"),)
+
+
+def split_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return tuple(
+        KernelVariant(name, f"{prefix}_{name}", num_warps=4,
+                      meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk, "SPLIT": split},
+                      default=name == SPLIT_DEFAULT, scratch_bytes=SPLIT_SCRATCH_BYTES)
+        for name, bm, bn, bk, split in SPLIT_TILES
+    )
+
+
 # Register-direct variants (conv_direct_fp32.hip): (variant id, BLOCK_M, BLOCK_N).
 DIRECT_SOURCE = "conv_direct_fp32.hip"
 DIRECT_TILES = (
@@ -93,37 +116,38 @@ def direct_variants(prefix: str) -> tuple[KernelVariant, ...]:
 
 
 def register_conv_family() -> None:
-    bn_inputs = tuple(
-        arg(name, "*fp32", "input", index=i)
-        for i, name in enumerate(("x", "weight", "scale", "bias", "mean", "variance"))
-    )
+    # conv_fp32.hip reads the weight as OHWI (a channel run of one tap is
+    # contiguous); conv_direct_fp32.hip reads OIHW.
+    def bn_inputs_for(weight_layout: str | None) -> tuple:
+        return tuple(
+            arg(name, "*fp32", "input", index=i, **({"layout": weight_layout} if i == 1 and weight_layout else {}))
+            for i, name in enumerate(("x", "weight", "scale", "bias", "mean", "variance"))
+        )
     epsilon = arg("epsilon", "fp32", "attribute_f64", name="batchnorm_epsilon", default=1e-5)
-    for op_type, kernel_id, prefix, inputs in (
-        ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw", "conv_bn_relu_fp32", bn_inputs),
-        ("FusedConvBatchNorm", "conv_bn.fp32.nchw", "conv_bn_fp32", bn_inputs),
-        (
-            "FusedConvBatchNormAddRelu",
-            "conv_bn_add_relu.fp32.nchw",
-            "conv_bn_add_relu_fp32",
-            bn_inputs + (arg("residual", "*fp32", "input", index=6),),
-        ),
+    families = ((CONV_SOURCE, "mfma", conv_variants, CONV_GRID, "OHWI"),
+                (CONV_SOURCE, "splitk", split_variants, SPLIT_GRID, "OHWI"),
+                (DIRECT_SOURCE, "direct", direct_variants, CONV_GRID, None))
+    residual = (arg("residual", "*fp32", "input", index=6),)
+    for op_type, kernel_id, prefix, extra in (
+        ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw", "conv_bn_relu_fp32", ()),
+        ("FusedConvBatchNorm", "conv_bn.fp32.nchw", "conv_bn_fp32", ()),
+        ("FusedConvBatchNormAddRelu", "conv_bn_add_relu.fp32.nchw", "conv_bn_add_relu_fp32", residual),
     ):
-        arguments = inputs + (arg("output", "*fp32", "output", index=0),) + CONV_DIMENSIONS + (epsilon,) + reserved()
-        for source, suffix, variants, grid in ((CONV_SOURCE, "mfma", conv_variants(prefix), CONV_GRID),
-                                               (DIRECT_SOURCE, "direct", direct_variants(prefix), CONV_GRID)):
+        for source, suffix, variants, grid, weight_layout in families:
+            inputs = bn_inputs_for(weight_layout) + extra
+            arguments = inputs + (arg("output", "*fp32", "output", index=0),) + CONV_DIMENSIONS + (epsilon,) + reserved()
             register(KernelSpec(
-                f"{kernel_id}.{suffix}", op_type, 1, source, arguments, grid, variants,
+                f"{kernel_id}.{suffix}", op_type, 1, source, arguments, grid, variants(prefix),
                 layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},),
             ))
-    conv_arguments = (
-        arg("x", "*fp32", "input", index=0),
-        arg("weight", "*fp32", "input", index=1),
-        arg("output", "*fp32", "output", index=0),
-    ) + CONV_DIMENSIONS + reserved()
-    for source, suffix, variants, grid in ((CONV_SOURCE, "mfma", conv_variants("conv_fp32"), CONV_GRID),
-                                           (DIRECT_SOURCE, "direct", direct_variants("conv_fp32"), CONV_GRID)):
+    for source, suffix, variants, grid, weight_layout in families:
+        conv_arguments = (
+            arg("x", "*fp32", "input", index=0),
+            arg("weight", "*fp32", "input", index=1, **({"layout": weight_layout} if weight_layout else {})),
+            arg("output", "*fp32", "output", index=0),
+        ) + CONV_DIMENSIONS + reserved()
         register(KernelSpec(
-            f"conv.fp32.nchw.{suffix}", "Conv", 1, source, conv_arguments, grid, variants,
+            f"conv.fp32.nchw.{suffix}", "Conv", 1, source, conv_arguments, grid, variants("conv_fp32"),
             layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},),
         ))
 

@@ -10,11 +10,12 @@
 // Argument order per entry point is the pack ABI order of resnet.py:242-300
 // and 382-400, with two trailing reserved pointers.
 //
-// GEMM view of a convolution (NCHW input, OIHW weights):
+// GEMM view of a convolution (NCHW input; the OIHW weight is read as its OHWI copy):
 //   rows    m = output channel                        (K_out)
 //   columns j = image * P*Q + output pixel            (N*P*Q)
-//   depth   d = (input channel, kernel row, kernel column)   (C*R*S)
-//   A[m][d] = W[m][c][r][s]  (OIHW is already row-major [K_out, C*R*S])
+//   depth   d = (kernel row, kernel column, input channel)   (R*S*C)
+//   A[m][d] = W[m][r][s][c]  (the weight arrives as OHWI, row-major
+//                             [K_out, R*S*C]: d = (r*S + s)*C + c)
 //   B[d][j] = X[n][c][oh*sh - ph + r*dh][ow*sw - pw + s*dw]   (zero padded)
 //
 // Tiling. A workgroup (4 wavefronts) computes a BM x BN output tile and
@@ -23,6 +24,17 @@
 // WGM x WGN x WGK grid: each owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA
 // accumulators over 1/WGK of every depth tile; WGK > 1 partial sums are added
 // through LDS before the epilogue.
+//
+// Split-K (SPLIT > 1): the grid carries SPLIT workgroups per output tile,
+// each accumulating an equal share of the depth tiles. Every share is written
+// to the runtime scratch with agent-coherent stores; after the stores have
+// completed, one atomic increment of the tile's counter tells the workgroup
+// whether it is the last of the tile. The last one reads all shares back and
+// adds them in split order (0, 1, ..., SPLIT-1: the result does not depend on
+// arrival order),
+// applies the epilogue and resets the counter to zero for the next launch.
+// Nothing waits on another workgroup, and no cache-wide write-back is needed:
+// only the shares travel through the coherent level.
 //
 // LDS holds both operands depth-contiguous, A as [m][d] and B as [j][d]
 // (rows padded by 4 floats), so one 16-byte read gives a lane four depths.
@@ -68,9 +80,30 @@ __device__ __forceinline__ float LoadF32(__amdgpu_buffer_rsrc_t r, int byte_offs
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 0));
 }
 
+// Per-lane byte offset plus a wave-uniform one (kept in a scalar register).
+// With byte_offset = kNoRead the sum stays at or above 2^31 (the uniform part
+// is below 2^31), so the element still reads 0.
+__device__ __forceinline__ float LoadF32(__amdgpu_buffer_rsrc_t r, int byte_offset, int uniform_offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, uniform_offset, 0));
+}
+
 __device__ __forceinline__ f32x4 LoadF32x4(__amdgpu_buffer_rsrc_t r, int byte_offset) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
+// Runtime scratch of the split-K variants: one counter per output tile, then
+// the shares, [tile][split][BM*BN] floats in accumulator-register order.
+constexpr int kSplitMaxTiles = 16384;
+constexpr long long kSplitCounterBytes = kSplitMaxTiles * 4LL;
+constexpr long long kSplitShareBytes = 128LL << 20;
+
+// Agent-coherent (sc1) 32-bit accesses for the split-K shares and counters.
+__device__ __forceinline__ void StoreShared(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float LoadShared(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // LDS layout of one ConvCore instantiation (in floats).
@@ -88,12 +121,14 @@ struct ConvLds {
 
 // POINTWISE: 1x1 kernel without padding, so every gathered pixel is inside
 // the image and a depth row is one input channel.
-template <int BM, int BN, int BK, int WGM, int WGN, int WGK, int EPI, bool POINTWISE>
+template <int BM, int BN, int BK, int WGM, int WGN, int WGK, int EPI, bool POINTWISE, int SPLIT = 1,
+          bool CHANNEL_RUN = false>
 __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* __restrict__ x,
                                          const float* __restrict__ weight, const float* __restrict__ scale,
                                          const float* __restrict__ bias, const float* __restrict__ mean,
                                          const float* __restrict__ variance, const float* __restrict__ residual,
-                                         float* __restrict__ output, const ConvGeometry g, const float epsilon) {
+                                         float* __restrict__ output, const ConvGeometry g, const float epsilon,
+                                         void* __restrict__ scratch = nullptr) {
   using L = ConvLds<BM, BN, BK, WGM, WGN, WGK>;
   constexpr int WM = BM / WGM;
   constexpr int WN = BN / WGN;
@@ -108,6 +143,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   static_assert(TM >= 1 && TN >= 1 && WAVE_GROUPS >= 1, "wave tile too small");
   static_assert(A_CHUNKS >= 1 && A_CHUNKS * kThreads * 4 == BM * BK, "A tile split");
   static_assert(kThreads % BN == 0 && B_RUN % 4 == 0, "B tile split");
+  static_assert(SPLIT == 1 || WGK == 1, "split-K variants keep the depth whole inside a workgroup");
 
   float* a_tile = smem;                  // [2][BM][ROW]
   float* b_tile = smem + 2 * L::kA;      // [2][BN][ROW]
@@ -173,10 +209,63 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     pw_base = img * g.c * hw + (oh * g.stride_h) * g.w + ow * g.stride_w;
   };
 
-  f32x4 ra[A_CHUNKS];
-  float rb[B_RUN];
+  // Register staging of one depth tile between its global loads and its LDS
+  // store (the next tile's loads are in flight during the current MFMAs).
+  struct Stage {
+    f32x4 a[A_CHUNKS];
+    float b[B_RUN];
+  };
+  Stage st0;
 
-  auto load_tile = [&](int d0) {
+  // Channel-run depth order (CHANNEL_RUN, C % BK == 0): depth tile t holds
+  // channels [c0, c0 + BK) of one kernel tap (r, s); tiles take c fastest,
+  // then s, then r. Inside a tile the tap is fixed, so a B element needs no
+  // index arithmetic and the padding test is made once per tile. The loads
+  // always come in increasing tile order, so the tap walks forward.
+  int run_c0 = 0, run_r = 0, run_s = 0;  // next tile to load
+  auto seek_run = [&](int kt) {
+    const int per_tap = g.c / BK;
+    const int tap = kt / per_tap;
+    run_c0 = (kt - tap * per_tap) * BK;
+    run_r = tap / g.s;
+    run_s = tap - run_r * g.s;
+  };
+  auto load_run = [&](Stage& st) {
+    f32x4* ra = st.a;
+    float* rb = st.b;
+    const int tap = run_r * g.s + run_s;
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int m = m0 + chunk / (BK / 4);
+      const int c = run_c0 + (chunk % (BK / 4)) * 4;
+      // OHWI weight: the channels of one tap are contiguous.
+      ra[i] = LoadF32x4(w_res, m < g.k ? (m * depth + tap * g.c + c) * 4 : kNoRead);
+    }
+    const int dh = run_r * g.dil_h;
+    const int dw = run_s * g.dil_w;
+    const bool inside = col_ok && static_cast<unsigned>(ih0 + dh) < static_cast<unsigned>(g.h) &&
+                        static_cast<unsigned>(iw0 + dw) < static_cast<unsigned>(g.w);
+    const int off = inside ? (lane_base + (run_c0 + b_run0) * hw + dh * g.w + dw) * 4 : kNoRead;
+#pragma unroll
+    for (int e = 0; e < B_RUN; ++e) rb[e] = LoadF32(x_res, off, e * hw * 4);
+    run_c0 += BK;
+    if (run_c0 == g.c) {
+      run_c0 = 0;
+      if (++run_s == g.s) {
+        run_s = 0;
+        ++run_r;
+      }
+    }
+  };
+
+  auto load_tile = [&](Stage& st, int d0) {
+    if (CHANNEL_RUN) {
+      load_run(st);
+      return;
+    }
+    f32x4* ra = st.a;
+    float* rb = st.b;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
       const int chunk = tid + kThreads * i;
@@ -197,10 +286,11 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
         rb[e] = LoadF32(x_res, (col_ok && d + e < depth) ? (pw_base + (d + e) * hw) * 4 : kNoRead);
       }
     } else {
-      int ci = d / rs;
-      const int rr = d - ci * rs;
-      int kr = rr / g.s;
-      int ks = rr - kr * g.s;
+      // Depth order of an OHWI weight row: d = (kr * S + ks) * C + ci.
+      const int tap = d / g.c;
+      int ci = d - tap * g.c;
+      int kr = tap / g.s;
+      int ks = tap - kr * g.s;
 #pragma unroll
       for (int e = 0; e < B_RUN; ++e) {
         const int dh = kr * g.dil_h;
@@ -209,18 +299,20 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
                             static_cast<unsigned>(ih0 + dh) < static_cast<unsigned>(g.h) &&
                             static_cast<unsigned>(iw0 + dw) < static_cast<unsigned>(g.w);
         rb[e] = LoadF32(x_res, inside ? (lane_base + ci * hw + dh * g.w + dw) * 4 : kNoRead);
-        if (++ks == g.s) {
-          ks = 0;
-          if (++kr == g.r) {
-            kr = 0;
-            ++ci;
+        if (++ci == g.c) {
+          ci = 0;
+          if (++ks == g.s) {
+            ks = 0;
+            ++kr;
           }
         }
       }
     }
   };
 
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](const Stage& st, int buf) {
+    const f32x4* ra = st.a;
+    const float* rb = st.b;
     float* at = a_tile + buf * L::kA;
     float* bt = b_tile + buf * L::kB;
 #pragma unroll
@@ -244,6 +336,29 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   const int half = lane >> 5;
   const int lane32 = lane & 31;
 
+  // MFMAs of one LDS depth tile (buffer `cur`) into acc.
+  auto compute_tile = [&](int cur) {
+    const float* at = a_tile + cur * L::kA + (wm + lane32) * ROW + 4 * half;
+    const float* bt = b_tile + cur * L::kB + (wn + lane32) * ROW + 4 * half;
+#pragma unroll
+    for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
+      const int col = (wk * WAVE_GROUPS + gi) * 8;
+      f32x4 av[TM];
+      f32x4 bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const f32x4*>(at + i * 32 * ROW + col);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) bv[t] = *reinterpret_cast<const f32x4*>(bt + t * 32 * ROW + col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int t = 0; t < TN; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[t][e], acc[i][t], 0, 0, 0);
+    }
+  };
+
   // Accumulates depth tiles [kb, ke) of the current output tile into acc.
   // Ends with a barrier, after which the LDS tiles are free.
   auto run_depth = [&](int kb, int ke) {
@@ -253,33 +368,16 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
       for (int t = 0; t < TN; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][t][r] = 0.0f;
-    load_tile(kb * BK);
-    store_tile(0);
+    if (CHANNEL_RUN) seek_run(kb);
+    load_tile(st0, kb * BK);
+    store_tile(st0, 0);
     __syncthreads();
     for (int kt = kb; kt < ke; ++kt) {
       const int cur = (kt - kb) & 1;
       const bool more = kt + 1 < ke;
-      if (more) load_tile((kt + 1) * BK);
-      const float* at = a_tile + cur * L::kA + (wm + lane32) * ROW + 4 * half;
-      const float* bt = b_tile + cur * L::kB + (wn + lane32) * ROW + 4 * half;
-#pragma unroll
-      for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
-        const int col = (wk * WAVE_GROUPS + gi) * 8;
-        f32x4 av[TM];
-        f32x4 bv[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const f32x4*>(at + i * 32 * ROW + col);
-#pragma unroll
-        for (int t = 0; t < TN; ++t) bv[t] = *reinterpret_cast<const f32x4*>(bt + t * 32 * ROW + col);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int t = 0; t < TN; ++t)
-              acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[t][e], acc[i][t], 0, 0, 0);
-      }
-      if (more) store_tile(cur ^ 1);
+      if (more) load_tile(st0, (kt + 1) * BK);
+      compute_tile(cur);
+      if (more) store_tile(st0, cur ^ 1);
       __syncthreads();
     }
   };
@@ -319,8 +417,79 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     }
   };
 
-  setup_tile(ct::XcdContiguousIndex(blockIdx.x + blockIdx.y * gridDim.x, tiles));
-  run_depth(0, depth_tiles);
+  if (SPLIT == 1) {
+    setup_tile(ct::XcdContiguousIndex(blockIdx.x + blockIdx.y * gridDim.x, tiles));
+    run_depth(0, depth_tiles);
+  } else {
+    // Grid (tiles_n, tiles_m, SPLIT); the shares of one tile get adjacent
+    // slots, so they run on one XCD at about the same time.
+    const int linear = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int slot = ct::XcdContiguousIndex(linear, tiles * SPLIT);
+    const int tile = slot / SPLIT;
+    const int split = slot - tile * SPLIT;
+    const bool fits = tiles <= kSplitMaxTiles &&
+                      static_cast<long long>(tiles) * SPLIT * BM * BN * 4 <= kSplitShareBytes;
+    if (!fits) {
+      // Scratch too small for this shape: share 0 computes the whole depth.
+      if (split != 0) return;
+      setup_tile(tile);
+      run_depth(0, depth_tiles);
+    } else {
+      const int per = (depth_tiles + SPLIT - 1) / SPLIT;
+      const int kb = min(depth_tiles, split * per);
+      const int ke = min(depth_tiles, kb + per);
+      setup_tile(tile);
+      run_depth(kb, ke);
+      unsigned* counters = static_cast<unsigned*>(scratch);
+      float* shares = reinterpret_cast<float*>(static_cast<char*>(scratch) + kSplitCounterBytes) +
+                      static_cast<size_t>(tile) * SPLIT * BM * BN;
+      constexpr int WAVE_REGS = TM * TN * 16 * 64;  // one wavefront's accumulators
+      float* mine = shares + static_cast<size_t>(split) * BM * BN + wave * WAVE_REGS;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) StoreShared(mine + ((i * TN + t) * 16 + r) * 64 + lane, acc[i][t][r]);
+      // The shares must have reached the coherent level before the count.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      unsigned* flag = reinterpret_cast<unsigned*>(smem);
+      if (tid == 0) {
+        const unsigned arrived = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+        *flag = arrived;
+      }
+      __syncthreads();
+      const unsigned arrived = *flag;
+      if (arrived != SPLIT - 1) return;
+      if (tid == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Sum all shares in split order from the scratch (this workgroup's own
+      // share is there too, stored and completed above).
+      // The 16 loads of one accumulator per share are issued together so
+      // that their latencies overlap.
+      const float* base = shares + wave * WAVE_REGS + lane;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const float* block = base + (i * TN + t) * 16 * 64;
+          float sum[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sum[r] = LoadShared(block + r * 64);
+#pragma unroll
+          for (int sp = 1; sp < SPLIT; ++sp) {
+            float part[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[r] = LoadShared(block + static_cast<size_t>(sp) * BM * BN + r * 64);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sum[r] += part[r];
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][t][r] = sum[r];
+        }
+    }
+  }
 
   // ---- Depth-split partial sums: wavefronts wk > 0 add theirs to wk == 0
   // through LDS (register r of lane l lands at [slot][r][l]).
@@ -372,15 +541,19 @@ __device__ __forceinline__ ConvGeometry MakeGeometry(int n, int c, int h, int w,
   MakeGeometry(n, c, h, w, k, r, s, out_h, out_w, stride_h, stride_w, pad_h, pad_w, dilation_h, dilation_w)
 
 // One LDS buffer per kernel, shared by the pointwise and general paths.
-#define CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, EPI, ...)                                             \
+// Loader choice: channel runs when C is a multiple of the depth tile, else
+// the pointwise gather for unpadded 1x1, else the general (c, r, s) walk.
+#define CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, EPI, ...)                                         \
   __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];  \
-  if (r == 1 && s == 1 && pad_h == 0 && pad_w == 0) {                                               \
-    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, true>(smem, __VA_ARGS__);                              \
+  if (c % BK == 0) {                                                                                \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, false, 1, true>(smem, __VA_ARGS__);                \
+  } else if (r == 1 && s == 1 && pad_h == 0 && pad_w == 0) {                                        \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, true>(smem, __VA_ARGS__);                       \
   } else {                                                                                          \
-    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, false>(smem, __VA_ARGS__);                             \
+    ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, false>(smem, __VA_ARGS__);                      \
   }
 
-#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                          \
+#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                      \
   CT_KERNEL void __launch_bounds__(kThreads) conv_bn_relu_fp32_##NAME(                                  \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
@@ -413,6 +586,50 @@ CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2)
 CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2)
 CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
 
+// Split-K entry points: the first reserved argument is the runtime scratch
+// (kSplitCounterBytes + kSplitShareBytes, zero-initialised by the engine).
+#define CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, EPI, ...)                                 \
+  __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, 1>::kFloats];    \
+  if (c % BK == 0) {                                                                                \
+    ConvCore<BM, BN, BK, WGM, WGN, 1, EPI, false, SPLIT, true>(smem, __VA_ARGS__);              \
+  } else if (r == 1 && s == 1 && pad_h == 0 && pad_w == 0) {                                        \
+    ConvCore<BM, BN, BK, WGM, WGN, 1, EPI, true, SPLIT>(smem, __VA_ARGS__);                     \
+  } else {                                                                                          \
+    ConvCore<BM, BN, BK, WGM, WGN, 1, EPI, false, SPLIT>(smem, __VA_ARGS__);                    \
+  }
+
+#define CT_DEFINE_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT)                                   \
+  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_relu_fp32_##NAME(                                  \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
+      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
+    CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormRelu, x, weight, scale, bias, mean,         \
+                      variance, nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                     \
+  }                                                                                                      \
+  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_fp32_##NAME(                                       \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
+      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
+    CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNorm, x, weight, scale, bias, mean, variance,   \
+                      nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                               \
+  }                                                                                                      \
+  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_add_relu_fp32_##NAME(                              \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
+      const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon,          \
+      void* scratch, void*) {                                                                            \
+    CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormAddRelu, x, weight, scale, bias, mean,      \
+                      variance, residual, output, CT_CONV_GEOMETRY, epsilon, scratch)                    \
+  }                                                                                                      \
+  CT_KERNEL void __launch_bounds__(kThreads) conv_fp32_##NAME(const float* x, const float* weight,      \
+                                                              float* output, CT_CONV_DIMS, void* scratch, \
+                                                              void*) {                                   \
+    CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr, \
+                      nullptr, output, CT_CONV_GEOMETRY, 0.0f, scratch)                                  \
+  }
+
+// name, BM, BN, BK, WGM, WGN, SPLIT
+CT_DEFINE_SPLIT_VARIANTS(m128n128s2, 128, 128, 32, 2, 2, 2)
+CT_DEFINE_SPLIT_VARIANTS(m128n128s4, 128, 128, 32, 2, 2, 4)
+CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8)
+
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one
 // 1 x n "image").
@@ -421,15 +638,26 @@ CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
                                                               int m, int n, int k, void*, void*) {        \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
-    ConvCore<BM, BN, BK, WGM, WGN, WGK, kPlain, true>(smem, b, a, nullptr, nullptr, nullptr, nullptr,     \
-                                                      nullptr, output, g, 0.0f);                          \
+    if (k % BK == 0) {                                                                                    \
+      ConvCore<BM, BN, BK, WGM, WGN, WGK, kPlain, false, 1, true>(smem, b, a, nullptr, nullptr, nullptr, \
+                                                                     nullptr, nullptr, output, g, 0.0f);  \
+    } else {                                                                                              \
+      ConvCore<BM, BN, BK, WGM, WGN, WGK, kPlain, true>(smem, b, a, nullptr, nullptr, nullptr, nullptr,   \
+                                                        nullptr, output, g, 0.0f);                        \
+    }                                                                                                     \
   }                                                                                                       \
   CT_KERNEL void __launch_bounds__(kThreads) gemm_bias_fp32_##NAME(                                      \
       const float* a, const float* b, const float* bias, float* output, int m, int n, int k, void*, void*) { \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
-    ConvCore<BM, BN, BK, WGM, WGN, WGK, kColumnBias, true>(smem, b, a, nullptr, bias, nullptr, nullptr,   \
-                                                           nullptr, output, g, 0.0f);                     \
+    if (k % BK == 0) {                                                                                    \
+      ConvCore<BM, BN, BK, WGM, WGN, WGK, kColumnBias, false, 1, true>(smem, b, a, nullptr, bias,      \
+                                                                          nullptr, nullptr, nullptr,      \
+                                                                          output, g, 0.0f);               \
+    } else {                                                                                              \
+      ConvCore<BM, BN, BK, WGM, WGN, WGK, kColumnBias, true>(smem, b, a, nullptr, bias, nullptr, nullptr, \
+                                                             nullptr, output, g, 0.0f);                   \
+    }                                                                                                     \
   }
 
 CT_DEFINE_GEMM_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)

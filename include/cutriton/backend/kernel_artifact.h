@@ -42,7 +42,17 @@ struct KernelArgumentSource {
   int attribute_index{0};
   int64_t default_int{0};
   double default_float{0.0};
+  // "input" only: the kernel reads this input in another memory layout of
+  // the same logical shape. "OHWI" (a constant OIHW weight stored as
+  // [out][kh][kw][in]) is the one layout defined; the engine keeps the
+  // re-laid-out copy of the constant beside the original.
+  std::string layout;
 };
+
+// Name of the re-laid-out copy of constant `name` in `layout`.
+inline std::string LaidOutConstantName(const std::string& name, const std::string& layout) {
+  return name + "#" + layout;
+}
 
 struct KernelArgumentSpec {
   std::string name;

@@ -441,6 +441,24 @@ void KernelPackAbi() {
       ++g_failures;
     }
   }
+  // Input layouts: OHWI on an input is accepted; any other layout, or a
+  // layout on an output, is rejected.
+  auto with_source = [&](const std::string& from, const std::string& to) {
+    std::string text = PackText(2, v2_grid);
+    text.replace(text.find(from), from.size(), to);
+    return text;
+  };
+  const std::string x_source = R"("source": {"kind": "input", "index": 0})";
+  const std::string y_source = R"("source": {"kind": "output", "index": 0})";
+  write(with_source(x_source, R"("source": {"kind": "input", "index": 0, "layout": "OHWI"})"));
+  EXPECT_OK(repo.Load({root.string()}));
+  if (!repo.artifacts().empty()) EXPECT(repo.artifacts().front().arguments[0].source.layout == "OHWI");
+  EXPECT(LaidOutConstantName("w", "OHWI") == "w#OHWI");
+  write(with_source(x_source, R"("source": {"kind": "input", "index": 0, "layout": "NHWC"})"));
+  EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
+  write(with_source(y_source, R"("source": {"kind": "output", "index": 0, "layout": "OHWI"})"));
+  EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
+
   // Too deep a grid tree (depth 9).
   std::string deep = R"({"kind":"literal","value":1})";
   for (int i = 0; i < 9; ++i) deep = R"({"kind":"mul","args":[)" + deep + R"(,{"kind":"literal","value":1}]})";

@@ -20,6 +20,7 @@ from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant
 pytestmark = pytest.mark.gpu
 
 CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
+                 "splitk:m128n128s2", "splitk:m128n128s4", "splitk:m128n128s8",
                  "direct:d64n256", "direct:d64n64", "direct:d32n64")
 GEMM16_VARIANTS = ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64")
 
@@ -61,6 +62,11 @@ CONV_SHAPES = [
     (2, 20, 7, 7, 72, 1, 1, 0, 1),       # 1x1, P*Q = 49 straddles tile columns
     (1, 3, 31, 29, 16, 7, 2, 3, 1),      # stem-like: C*R*S = 147 (scalar weight loads)
     (1, 8, 12, 12, 24, 3, 1, 2, 2),      # dilation 2
+    # C a multiple of the depth tile: the channel-run loader
+    (2, 64, 9, 11, 40, 3, 2, 1, 1),      # stride 2, ragged tiles
+    (1, 64, 12, 12, 24, 3, 1, 2, 2),     # dilation 2, padding 2
+    (2, 64, 14, 14, 72, 1, 2, 0, 1),     # strided 1x1 (downsample)
+    (1, 48, 10, 10, 20, 3, 1, 1, 1),     # C = 48: channel runs only for 16-deep tiles
 ]
 
 
@@ -84,6 +90,35 @@ def test_conv_family_variants(tmp_path, family_variant, tail, kernel_base):
         assert len(ops) == 1 and ops[0].candidates[ops[0].selected_candidate].endswith(f"{kernel_id}:{variant}"), ops
         want = oracle.evaluate(g, feeds)[g.outputs[0]]
         assert_close_fp32(out[g.outputs[0]], want, what=f"{kernel_id}:{variant} {shape}")
+
+
+@pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8"])
+def test_split_k_shares_follow_the_inputs(tmp_path, variant):
+    """Split-K partial sums travel through the runtime scratch and the tile
+    counters reset themselves: consecutive launches on one context with
+    different inputs each match the oracle (a stale share or counter from the
+    previous launch would not), also under hipGraph replay."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    kernel_id = "conv_bn_relu.fp32.nchw.splitk"
+    pack = filtered_pack(tmp_path / "pack", only_kernel_variant(kernel_id, variant, "conv_bn_relu.fp32.nchw"))
+    g, feeds_a = conv_graph(rng, 2, 256, 14, 14, 256, 3, 1, 1, 1, tail="relu")
+    feeds_b = {"x": rng.standard_normal(feeds_a["x"].shape, dtype=np.float32) * 3.0}
+    eng = engine.build_engine(workloads.to_model(g), engine.CompileOptions(kernel_artifact_dir=pack,
+                                                                           tuning_mode="disabled"))
+    assert eng.ops()[0].candidates[eng.ops()[0].selected_candidate].endswith(f"{kernel_id}:{variant}")
+    ctx = eng.create_execution_context()
+    x = torch.empty(feeds_a["x"].shape, device="cuda:0")
+    shape, _ = eng.value_desc(g.outputs[0])
+    y = torch.empty(shape, device="cuda:0")
+    ctx.bind_input("x", x)
+    ctx.bind_output(g.outputs[0], y, layout="NCHW")
+    want = {"a": oracle.evaluate(g, feeds_a)[g.outputs[0]], "b": oracle.evaluate(g, feeds_b)[g.outputs[0]]}
+    for which in ("a", "b", "b", "a", "b"):
+        x.copy_(torch.from_numpy((feeds_a if which == "a" else feeds_b)["x"]))
+        ctx.run()
+        assert_close_fp32(y.cpu().numpy(), want[which], what=f"{variant} input {which}")
 
 
 @pytest.mark.parametrize("op", ["BatchNormalization", "Relu", "Add", "AddRelu"])

@@ -124,6 +124,19 @@ def test_rejects_non_identifier_symbols_and_bad_wave_counts():
         _spec(variants=(KernelVariant("v", "relu_fp32", num_warps=32, default=True),)).validate()
 
 
+def test_input_layout_is_checked():
+    spec = _spec()
+    laid_out = (ArgumentSpec("x", "*fp32", {"kind": "input", "index": 0, "layout": "OHWI"}),) + spec.arguments[1:]
+    _spec(arguments=laid_out).validate()
+    bad = (ArgumentSpec("x", "*fp32", {"kind": "input", "index": 0, "layout": "NHWC"}),) + spec.arguments[1:]
+    with pytest.raises(ValueError, match="layout"):
+        _spec(arguments=bad).validate()
+    on_output = spec.arguments[:1] + (ArgumentSpec("output", "*fp32", {"kind": "output", "index": 0,
+                                                                       "layout": "OHWI"}),) + spec.arguments[2:]
+    with pytest.raises(ValueError, match="unknown source field"):
+        _spec(arguments=on_output).validate()
+
+
 def test_elf_symbol_reader_rejects_non_elf():
     with pytest.raises(ValueError):
         builder.elf_function_symbols(b"// ptx\n")
