@@ -91,16 +91,17 @@ bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const Val
   for (const auto& name : node.outputs()) {
     if (!layout_ok(name)) return false;
   }
-  // An input read in another layout must be a rank-4 FP32 constant: the
-  // engine re-lays it out once, at constant upload.
+  // An input read in another layout must be a constant (the engine re-lays
+  // it out once, at constant upload): rank-4 FP32 for OHWI, rank 2 for NK.
   for (const auto& argument : artifact.arguments) {
     const KernelArgumentSource& s = argument.source;
     if (s.layout.empty()) continue;
     if (s.index < 0 || static_cast<std::size_t>(s.index) >= node.inputs().size()) return false;
     const ValueDesc* v = lookup(node.inputs()[static_cast<std::size_t>(s.index)]);
-    if (v == nullptr || !v->is_constant || v->tensor.shape.size() != 4 || v->tensor.dtype != DataType::kFloat32) {
-      return false;
-    }
+    if (v == nullptr || !v->is_constant) return false;
+    const bool ohwi = s.layout == "OHWI" && v->tensor.shape.size() == 4 && v->tensor.dtype == DataType::kFloat32;
+    const bool nk = s.layout == "NK" && v->tensor.shape.size() == 2;
+    if (!ohwi && !nk) return false;
   }
   for (const auto& c : artifact.constraints) {
     switch (c.kind) {

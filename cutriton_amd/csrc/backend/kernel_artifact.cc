@@ -140,8 +140,9 @@ KernelArgumentSpec ParseArgument(const Value& v) {
   s.default_float = DoubleOr(source, "default", 0.0);
   if (const Value* layout = source.find("layout")) {
     s.layout = layout->string();
-    if (s.kind != KernelArgumentSourceKind::kInput || s.layout != "OHWI") {
-      throw std::runtime_error("argument " + argument.name + ": only an input may request a layout, and only OHWI");
+    if (s.kind != KernelArgumentSourceKind::kInput || !IsInputLayout(s.layout)) {
+      throw std::runtime_error("argument " + argument.name +
+                               ": only an input may request a layout, and only OHWI or NK");
     }
   }
   return argument;

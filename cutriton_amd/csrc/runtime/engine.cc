@@ -339,30 +339,42 @@ class EngineState {
             if (device_constants.count(name) != 0) continue;
             const std::string base = name.substr(0, name.rfind('#'));
             const auto host = plan.constants().find(base);
-            if (host == plan.constants().end() || src.layout != "OHWI") {
+            if (host == plan.constants().end() || !IsInputLayout(src.layout)) {
               return Status::Internal("no constant to lay out as " + name);
             }
             const TensorDesc& desc = host->second.desc();
-            if (desc.shape.size() != 4 || desc.dtype != DataType::kFloat32) {
-              return Status::InvalidArgument("OHWI needs a rank-4 float32 constant: " + base);
-            }
-            const int64_t k = desc.shape[0], c = desc.shape[1], r = desc.shape[2], w = desc.shape[3];
             TensorDesc laid_out = desc;
-            laid_out.layout = "OHWI";
-            if (r * w == 1) {  // [K][C][1][1]: both orders are the same bytes
-              device_constants.emplace(name, Tensor(laid_out, device_constants.at(base).buffer(),
-                                                    device_constants.at(base).byte_offset()));
-              continue;
+            laid_out.layout = src.layout;
+            const auto* in_bytes =
+                static_cast<const std::uint8_t*>(host->second.buffer()->data()) + host->second.byte_offset();
+            std::vector<std::uint8_t> out(desc.ByteSize());
+            if (src.layout == "OHWI") {
+              if (desc.shape.size() != 4 || desc.dtype != DataType::kFloat32) {
+                return Status::InvalidArgument("OHWI needs a rank-4 float32 constant: " + base);
+              }
+              const int64_t k = desc.shape[0], c = desc.shape[1], r = desc.shape[2], w = desc.shape[3];
+              if (r * w == 1) {  // [K][C][1][1]: both orders are the same bytes
+                device_constants.emplace(name, Tensor(laid_out, device_constants.at(base).buffer(),
+                                                      device_constants.at(base).byte_offset()));
+                continue;
+              }
+              const auto* in = reinterpret_cast<const float*>(in_bytes);
+              auto* o = reinterpret_cast<float*>(out.data());
+              for (int64_t oc = 0; oc < k; ++oc)
+                for (int64_t i = 0; i < c; ++i)
+                  for (int64_t y = 0; y < r; ++y)
+                    for (int64_t x = 0; x < w; ++x)
+                      o[static_cast<std::size_t>(((oc * r + y) * w + x) * c + i)] =
+                          in[static_cast<std::size_t>(((oc * c + i) * r + y) * w + x)];
+            } else {  // NK: [K][N] -> [N][K], any element size
+              if (desc.shape.size() != 2) return Status::InvalidArgument("NK needs a rank-2 constant: " + base);
+              const int64_t kd = desc.shape[0], nd = desc.shape[1];
+              const std::size_t es = ElementSize(desc.dtype);
+              for (int64_t row = 0; row < kd; ++row)
+                for (int64_t col = 0; col < nd; ++col)
+                  std::memcpy(out.data() + static_cast<std::size_t>(col * kd + row) * es,
+                              in_bytes + static_cast<std::size_t>(row * nd + col) * es, es);
             }
-            const auto* in = reinterpret_cast<const float*>(static_cast<const std::uint8_t*>(host->second.buffer()->data()) +
-                                                            host->second.byte_offset());
-            std::vector<float> out(static_cast<std::size_t>(k * c * r * w));
-            for (int64_t o = 0; o < k; ++o)
-              for (int64_t i = 0; i < c; ++i)
-                for (int64_t y = 0; y < r; ++y)
-                  for (int64_t x = 0; x < w; ++x)
-                    out[static_cast<std::size_t>(((o * r + y) * w + x) * c + i)] =
-                        in[static_cast<std::size_t>(((o * c + i) * r + y) * w + x)];
             std::shared_ptr<Buffer> buffer;
             CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(desc.ByteSize(), device.id, &buffer));
             CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(out.data(), desc.ByteSize()));

@@ -20,9 +20,10 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Any
 
-# An input may ask for another layout of a constant of the same logical shape;
-# OHWI stores an OIHW convolution weight as [out][kh][kw][in].
-INPUT_LAYOUTS = frozenset({"OHWI"})
+# An input may ask for another layout of a constant of the same logical shape:
+# OHWI stores an OIHW convolution weight as [out][kh][kw][in]; NK stores a
+# [K, N] matrix transposed, as [N][K].
+INPUT_LAYOUTS = frozenset({"OHWI", "NK"})
 
 ARGUMENT_SOURCES: dict[str, frozenset[str]] = {
     "input": frozenset({"kind", "index", "layout"}),

@@ -1,5 +1,5 @@
-"""Pack entries of the FP16 FFN kernels (gemm_fp16.hip, layer_norm_fp16.hip,
-elementwise.hip).
+"""Pack entries of the FP16 FFN kernels (gemm_fp16.hip, gemm_fp16_nt.hip,
+layer_norm_fp16.hip, elementwise.hip).
 
 Argument order and sources follow the reference pack
 (``python/cutriton/triton_kernels/transformer.py:193-371``): Gemm/GemmGelu
@@ -52,6 +52,23 @@ GEMM_CONSTRAINTS = (
 )
 
 
+# Weight-transposed kernels (gemm_fp16_nt.hip): `b` is bound to the [N][K]
+# copy of a constant B (input layout NK). (variant id, BLOCK_M, BLOCK_N,
+# BLOCK_K, wavefronts)
+GEMM_NT_SOURCE = "gemm_fp16_nt.hip"
+GEMM_NT_TILES = (
+    ("m256n256w4", 256, 256, 64, 4),
+    ("m256n256w8", 256, 256, 64, 8),
+    ("m256n128w4", 256, 128, 64, 4),
+    ("m128n256w4", 128, 256, 64, 4),
+    ("m128n128w4", 128, 128, 64, 4),
+    ("m128n128k128w4", 128, 128, 128, 4),
+    ("m64n128w4", 64, 128, 64, 4),
+    ("m64n64w4", 64, 64, 64, 4),
+)
+GEMM_NT_DEFAULT = "m128n128w4"
+
+
 def gemm_variants(prefix: str) -> tuple[KernelVariant, ...]:
     return tuple(
         KernelVariant(
@@ -59,6 +76,16 @@ def gemm_variants(prefix: str) -> tuple[KernelVariant, ...]:
             meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk}, default=name == GEMM_DEFAULT,
         )
         for name, bm, bn, bk, waves in GEMM_TILES
+    )
+
+
+def gemm_nt_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return tuple(
+        KernelVariant(
+            name, f"{prefix}_{name}", num_warps=waves,
+            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk}, default=name == GEMM_NT_DEFAULT,
+        )
+        for name, bm, bn, bk, waves in GEMM_NT_TILES
     )
 
 
@@ -70,16 +97,24 @@ def register_gemms() -> None:
         ("gemm_gelu_bias.fp16.mfma", "GemmGelu", "gemm_gelu_bias_fp16", True),
     ):
         inputs = ("a", "b", "bias") if bias else ("a", "b")
-        arguments = tuple(arg(name, "*fp16", "input", index=i) for i, name in enumerate(inputs)) + (
-            arg("output", "*fp16", "output", index=0),
-        ) + GEMM_DIMS + reserved()
         constraints = ({"kind": "input_count_eq", "value": len(inputs)},) + GEMM_CONSTRAINTS
         if bias:
             constraints += ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)
-        register(KernelSpec(
-            kernel_id, op_type, 1, GEMM_SOURCE, arguments, GEMM_GRID, gemm_variants(prefix),
-            dtype="float16", constraints=constraints,
-        ))
+        # The weight-transposed family comes first in the pack (kernel ids sort
+        # that way), so its default is the untuned choice whenever B is a
+        # constant; "_kn" kernels read B as it is and serve every other Gemm.
+        for suffix, source, variants, b_source in (
+            ("", GEMM_NT_SOURCE, gemm_nt_variants(prefix.replace("_fp16", "_nt_fp16")), {"layout": "NK"}),
+            ("_kn", GEMM_SOURCE, gemm_variants(prefix), {}),
+        ):
+            arguments = tuple(
+                arg(name, "*fp16", "input", index=i, **(b_source if name == "b" else {}))
+                for i, name in enumerate(inputs)
+            ) + (arg("output", "*fp16", "output", index=0),) + GEMM_DIMS + reserved()
+            register(KernelSpec(
+                kernel_id + suffix, op_type, 1, source, arguments, GEMM_GRID, variants,
+                dtype="float16", constraints=constraints,
+            ))
 
 
 def register_elementwise() -> None:

@@ -1,0 +1,361 @@
+// FP16 Gemm / GemmGelu (+bias) on CDNA4 FP16 MFMA (v_mfma_f32_16x16x32_f16)
+// with FP32 accumulation, reading the weight operand from its transposed
+// copy.
+//
+// Semantics follow python/cutriton/triton_kernels/transformer.py:
+//   gemm_fp16 (17-60): Y = fp16(sum_k A[m,k] * B[k,n]) with FP32 accumulation;
+//   gemm_gelu_fp16 (63-107): Y = fp16(0.5 a (1 + erf(a / sqrt 2))), a the FP32 sum.
+// The bias entry points add bias[n] (FP16 widened to FP32) to the FP32 sum
+// before the activation. Argument order is the pack ABI of
+// transformer.py:256-271 (a, b, [bias,] output, m, n, k, two reserved); the
+// engine binds `b` to the [N][K] copy of the constant weight B[K][N], made
+// once at constant upload.
+//
+// With both operands depth-contiguous ([M][K] and [N][K]) every global load
+// is a 16-byte run of 8 depths, and so is every MFMA operand fragment: the
+// tile goes from global memory to LDS and from LDS to the MFMA without any
+// reordering.
+//
+// Pipeline. A workgroup owns a BM x BN output tile and walks the depth in
+// BK-deep tiles through a ring of STAGES LDS stages. The loads of tile
+// kt + STAGES - 1 are issued (straight into LDS, with buffer_load ... lds)
+// before tile kt is multiplied, so STAGES - 1 tiles are in flight behind the
+// MFMAs. One barrier per depth tile orders reuse of a stage.
+//
+// LDS layout. A stage holds BM A rows then BN B rows of BK halves, i.e.
+// CH = BK / 8 chunks of 16 bytes per row. Chunk c of row r sits at chunk
+// position c ^ f(r), f(r) = (r / (16 / CH)) % CH. An LDS read of 16 bytes per
+// lane is served 16 lanes at a time over 64 banks (256 bytes); the 16 lanes
+// of one phase read one logical chunk of 16 consecutive rows, and f makes
+// their (row mod (16 / CH), position) pairs - hence their banks - distinct.
+// (CH = 16: f(r) = r % 16, every row starts at bank 0.)
+//
+// MFMA. v_mfma_f32_16x16x32_f16 sustains a higher rate on gfx950 than the
+// 32x32x16 form. A lane's operand fragment is 8 consecutive depths (one
+// 16-byte chunk) of row lane % 16: depths 8 * (lane / 16) + 0..7 of the
+// 32-deep step.
+//
+// Operand roles. The MFMA takes the weight fragment as its row operand and
+// the activation fragment as its column operand, so it produces the
+// transposed 16x16 tile: a lane holds one output row m (lane % 16) and the
+// four consecutive columns n = 4 * (lane / 16) + 0..3 in its four registers.
+// The epilogue therefore stores 8 contiguous bytes per lane and tile.
+#include "common.h"
+
+namespace {
+
+using ct::f16x8;
+using ct::f32x4;
+using ct::u32x4;
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBufferFlags = 0x00020000;  // gfx9-family raw 32-bit buffer
+constexpr int kNoRead = 0x80000000;       // at or beyond every resource's range: reads 0
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+#define CT_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt immediate: vmcnt = n (6 bits, split over [3:0] and [15:14]),
+// expcnt and lgkmcnt at their maximum (no wait on them).
+template <int N>
+__device__ __forceinline__ void WaitVmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070 | 0x0F00);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t HalfResource(const _Float16* base, long long elements) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(base), 0, static_cast<int>(elements * 2),
+                                           kBufferFlags);
+}
+
+// Eight halves of row `row`, depths [col, col + 8), zero outside the matrix.
+// `ld` is the row length (= depth k); used when k is not a multiple of 8.
+__device__ __forceinline__ u32x4 LoadChunkScalar(const _Float16* base, int row, int rows, int col, int ld) {
+  _Float16 h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    h[e] = (row < rows && col + e < ld) ? base[static_cast<size_t>(row) * ld + col + e] : static_cast<_Float16>(0.0f);
+  }
+  u32x4 v;
+  __builtin_memcpy(&v, h, 16);
+  return v;
+}
+
+// erf-GELU in FP32 without exp and without branches:
+//   GELU(a) = a * Phi(a) = max(a, 0) - |a| * Q(|a|),  Q(x) = erfc(x / sqrt 2) / 2.
+// erfc follows Abramowitz & Stegun, Handbook of Mathematical Functions,
+// formula 7.1.28: erfc(z) = 1 / (1 + a1 z + ... + a6 z^6)^16 for z >= 0,
+// absolute error at most 3e-7. The polynomial is evaluated in x = z * sqrt 2
+// (coefficients a_i / sqrt(2)^i). For large x the 16th power overflows to
+// +inf and its reciprocal is 0, so GELU(a) = max(a, 0) there. FP32
+// evaluation keeps the total absolute error below 1e-6.
+__device__ __forceinline__ float GeluErfAs(float a) {
+  const float x = __builtin_fabsf(a);
+  float p = 5.3829750e-06f;                   // a6 / sqrt(2)^6
+  p = __builtin_fmaf(p, x, 4.8889953e-05f);   // a5 / sqrt(2)^5
+  p = __builtin_fmaf(p, x, 3.8003575e-05f);   // a4 / sqrt(2)^4
+  p = __builtin_fmaf(p, x, 3.2776560e-03f);   // a3 / sqrt(2)^3
+  p = __builtin_fmaf(p, x, 2.1141006e-02f);   // a2 / sqrt(2)^2
+  p = __builtin_fmaf(p, x, 4.9867346e-02f);   // a1 / sqrt(2)
+  p = __builtin_fmaf(p, x, 1.0f);
+  p = p * p;
+  p = p * p;
+  p = p * p;
+  p = p * p;
+  const float q = __builtin_amdgcn_rcpf(p);  // erfc(x / sqrt 2)
+  // x * Q(x) is below 1e-50 from x = 16 on; the clamp keeps +inf finite there
+  // (inf * 0) so that GELU(+inf) = +inf.
+  return __builtin_fmaf(-0.5f * __builtin_fminf(x, 16.0f), q, __builtin_fmaxf(a, 0.0f));
+}
+
+template <int BM, int BN, int BK, int STAGES>
+struct NtShape {
+  static constexpr int kChunks = BK / 8;             // 16-byte chunks per row
+  static constexpr int kRowsPerLoad = 64 / kChunks;  // rows one wavefront load fills
+  static constexpr int kStageChunks = (BM + BN) * kChunks;
+  static constexpr int kLdsChunks = STAGES * kStageChunks;
+};
+
+// VEC: k is a multiple of 8, so every 16-byte chunk is 8 depths of one row
+// and the tiles load straight into LDS; otherwise chunks are assembled
+// element by element through registers.
+template <int BM, int BN, int BK, int STAGES, int WAVES_M, int WAVES_N, bool GELU, bool BIAS, bool VEC>
+__device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float16* __restrict__ a,
+                                           const _Float16* __restrict__ bt, const _Float16* __restrict__ bias,
+                                           _Float16* __restrict__ output, const int m, const int n, const int k) {
+  using S = NtShape<BM, BN, BK, STAGES>;
+  constexpr int CH = S::kChunks;
+  constexpr int RPL = S::kRowsPerLoad;
+  constexpr int WAVES = WAVES_M * WAVES_N;
+  constexpr int WM = BM / WAVES_M;
+  constexpr int WN = BN / WAVES_N;
+  constexpr int TM = WM / 16;
+  constexpr int TN = WN / 16;
+  constexpr int STEPS = BK / 32;
+  constexpr int LOADS = (BM + BN) / RPL / WAVES;  // load instructions per wavefront and tile
+  static_assert(BK == 64 || BK == 128, "depth tile of 2 or 4 MFMA steps");
+  static_assert(STAGES >= 2 && STAGES <= 4, "ring of 2..4 stages");
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 16x16 MFMA tile");
+  static_assert(LOADS * RPL * WAVES == BM + BN && BM % RPL == 0, "loads split evenly; none straddles A and B");
+  static_assert(2 * LOADS < 64, "vmcnt range");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  // Tile order: XCD-contiguous ranges, then groups of 8 row tiles walked
+  // column by column so that concurrently running tiles share A and B panels.
+  constexpr int GROUP_M = 8;
+  const int tiles_m = (m + BM - 1) / BM;
+  const int tiles_n = (n + BN - 1) / BN;
+  const int tile = ct::XcdContiguousIndex(blockIdx.x, tiles_m * tiles_n);
+  const int group_width = GROUP_M * tiles_n;
+  const int group = tile / group_width;
+  const int first_m = group * GROUP_M;
+  const int group_rows = min(tiles_m - first_m, GROUP_M);
+  const int within = tile - group * group_width;
+  const int m0 = (first_m + within % group_rows) * BM;
+  const int n0 = (within / group_rows) * BN;
+
+  const __amdgpu_buffer_rsrc_t a_res = HalfResource(a, static_cast<long long>(m) * k);
+  const __amdgpu_buffer_rsrc_t b_res = HalfResource(bt, static_cast<long long>(n) * k);
+
+  // Loader: wavefront load j of a tile fills rows [R0, R0 + RPL) with
+  // R0 = (j * WAVES + wave) * RPL; the hardware puts lane i's 16 bytes at
+  // chunk position i of that KiB, i.e. row R0 + i / CH, physical chunk
+  // i % CH, which holds logical chunk (i % CH) ^ f(row).
+  const int ld_row = lane / CH;
+  const int ld_pos = lane % CH;
+
+  auto load_tile = [&](int stage, int kt) {
+    u32x4* base = lds + stage * S::kStageChunks;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int r0 = (j * WAVES + wave) * RPL;  // wave-uniform
+      const int row = r0 + ld_row;
+      const int col = k0 + (ld_pos ^ ((row / (16 / CH)) % CH)) * 8;
+      const bool is_a = r0 < BM;
+      const int gr = is_a ? m0 + row : n0 + row - BM;
+      const int rows = is_a ? m : n;
+      if (VEC) {
+        const int offset = (col < k && gr < rows) ? (gr * k + col) * 2 : kNoRead;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? a_res : b_res, CT_LDS(base + r0 * CH), 16, offset, 0, 0, 0);
+      } else {
+        base[r0 * CH + lane] = LoadChunkScalar(is_a ? a : bt, gr, rows, col, k);
+      }
+    }
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][i][r] = 0.0f;
+
+  const int wm = (wave / WAVES_N) * WM;
+  const int wn = (wave % WAVES_N) * WN;
+  const int lane16 = lane & 15;
+  const int quarter = lane >> 4;
+  // Fragment rows are lane16 plus a multiple of 16, so f(row) = f(lane16).
+  const int a_row = (wm + lane16) * CH;
+  const int b_row = (BM + wn + lane16) * CH;
+  const int swz = (lane16 / (16 / CH)) % CH;
+
+  // MFMAs of one stage. The fragments of step s + 1 are read while the
+  // MFMAs of step s run; the scheduling groups at the end fix the order of
+  // the whole stage (first reads, then per step one LDS read after each of
+  // the first TM + TN MFMAs), so the read latency hides behind the matrix
+  // pipeline instead of stalling it.
+  auto compute_tile = [&](int stage) {
+    const u32x4* tile_base = lds + stage * S::kStageChunks;
+    f16x8 af[2][TM];
+    f16x8 bf[2][TN];
+    auto read_frags = [&](int step, f16x8* fa, f16x8* fb) {
+      const int chunk = (4 * step + quarter) ^ swz;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = __builtin_bit_cast(f16x8, tile_base[a_row + i * 16 * CH + chunk]);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) fb[t] = __builtin_bit_cast(f16x8, tile_base[b_row + t * 16 * CH + chunk]);
+    };
+    read_frags(0, af[0], bf[0]);
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step) {
+      const int cur_f = step & 1;
+      if (step + 1 < STEPS) read_frags(step + 1, af[cur_f ^ 1], bf[cur_f ^ 1]);
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[cur_f][t], af[cur_f][i], acc[t][i], 0, 0, 0);
+    }
+    constexpr int READS = TM + TN;
+    constexpr int MFMAS = TM * TN;
+    constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS, 0);
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step) {
+      if (step + 1 < STEPS) {
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+        if (READS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - PAIRS, 0);
+        if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS, 0);
+      }
+    }
+  };
+
+  // Waits until this wavefront's loads of tile kt have landed, `later` being
+  // the number of tiles issued after it (LOADS instructions each).
+  auto wait_tile = [&](int later) {
+    if (!VEC) return;  // the element-wise path stored synchronously
+    if (later >= 2) {
+      WaitVmcnt<2 * LOADS>();
+    } else if (later == 1) {
+      WaitVmcnt<LOADS>();
+    } else {
+      WaitVmcnt<0>();
+    }
+  };
+
+  const int k_tiles = (k + BK - 1) / BK;
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < k_tiles) load_tile(s, s);
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    wait_tile(min(STAGES - 2, k_tiles - 1 - kt));
+    // After the barrier every wavefront's loads of tile kt have landed and
+    // every wavefront is done with tile kt - 1, whose stage takes the next load.
+    __syncthreads();
+    if (kt + STAGES - 1 < k_tiles) load_tile((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+    compute_tile(kt % STAGES);
+  }
+
+  // Epilogue: lane holds row m = m0 + wm + 16 i + lane16 and columns
+  // n = n0 + wn + 16 t + 4 quarter + 0..3.
+  const bool vec_out = (n & 3) == 0;
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int col = n0 + wn + t * 16 + 4 * quarter;
+    if (col >= n) continue;
+    float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (BIAS) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias4[e] = col + e < n ? static_cast<float>(bias[col + e]) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm + i * 16 + lane16;
+      if (row >= m) continue;
+      f16x4 out4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[t][i][e];
+        if (BIAS) v += bias4[e];
+        if (GELU) v = GeluErfAs(v);
+        out4[e] = static_cast<_Float16>(v);
+      }
+      _Float16* dst = output + static_cast<size_t>(row) * n + col;
+      if (vec_out && col + 4 <= n) {
+        *reinterpret_cast<f16x4*>(dst) = out4;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e < n) dst[e] = out4[e];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Entry point body: one LDS allocation shared by the two loader paths.
+#define CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, GELU, BIAS, BIAS_PTR)                                  \
+  __shared__ u32x4 lds[NtShape<BM, BN, BK, ST>::kLdsChunks];                                           \
+  if ((k & 7) == 0) {                                                                                  \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, true>(lds, a, bt, BIAS_PTR, output, m, n, k);       \
+  } else {                                                                                             \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, false>(lds, a, bt, BIAS_PTR, output, m, n, k);      \
+  }
+
+#define CT_DEFINE_GEMM_NT(NAME, BM, BN, BK, ST, WM, WN)                                                     \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
+      gemm_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,     \
+                          void*, void*) {                                                                   \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, false, false, nullptr)                                          \
+  }                                                                                                         \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
+      gemm_gelu_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k, \
+                               void*, void*) {                                                              \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, true, false, nullptr)                                           \
+  }                                                                                                         \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
+      gemm_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,                 \
+                               _Float16* output, int m, int n, int k, void*, void*) {                       \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, false, true, bias)                                              \
+  }                                                                                                         \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
+      gemm_gelu_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,            \
+                                    _Float16* output, int m, int n, int k, void*, void*) {                  \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, true, true, bias)                                               \
+  }
+
+// name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N
+CT_DEFINE_GEMM_NT(m256n256w4, 256, 256, 64, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m256n256w8, 256, 256, 64, 2, 2, 4)
+CT_DEFINE_GEMM_NT(m256n128w4, 256, 128, 64, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m128n256w4, 128, 256, 64, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m128n128w4, 128, 128, 64, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m128n128k128w4, 128, 128, 128, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m64n128w4, 64, 128, 64, 2, 1, 4)
+CT_DEFINE_GEMM_NT(m64n64w4, 64, 64, 64, 2, 2, 2)

@@ -22,7 +22,11 @@ pytestmark = pytest.mark.gpu
 CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
                  "splitk:m128n128s2", "splitk:m128n128s4", "splitk:m128n128s8",
                  "direct:d64n256", "direct:d64n64", "direct:d32n64")
-GEMM16_VARIANTS = ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64")
+# (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
+# "_kn" reads B as it is.
+GEMM16_VARIANTS = tuple(("", v) for v in ("m256n256w4", "m256n256w8", "m256n128w4", "m128n256w4", "m128n128w4",
+                                          "m128n128k128w4", "m64n128w4", "m64n64w4")) + \
+    tuple(("_kn", v) for v in ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64"))
 
 
 def conv_graph(rng, n, c, h, w, k, r, stride, pad, dil, tail: str):
@@ -235,14 +239,25 @@ def gemm16_graph(rng, m, k, n, gelu, bias):
     return g, {"a": rng.standard_normal((m, k)).astype(np.float16)}
 
 
-@pytest.mark.parametrize("variant", GEMM16_VARIANTS)
+@pytest.mark.parametrize("family,variant", GEMM16_VARIANTS)
 @pytest.mark.parametrize("gelu,bias", [(False, False), (True, False), (False, True), (True, True)])
-def test_gemm_fp16_variants(tmp_path, variant, gelu, bias):
+def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
     rng = np.random.default_rng(13)
-    kid = {(False, False): "gemm.fp16.mfma", (True, False): "gemm_gelu.fp16.mfma",
-           (False, True): "gemm_bias.fp16.mfma", (True, True): "gemm_gelu_bias.fp16.mfma"}[(gelu, bias)]
-    pack = filtered_pack(tmp_path / "pack", only_variant(kid, variant))
-    for m, k, n in ((512, 768, 3072), (17, 128, 40), (70, 72, 37), (300, 200, 264)):
+    base = {(False, False): "gemm.fp16.mfma", (True, False): "gemm_gelu.fp16.mfma",
+            (False, True): "gemm_bias.fp16.mfma", (True, True): "gemm_gelu_bias.fp16.mfma"}[(gelu, bias)]
+    kid = base + family
+    sibling = base + ("_kn" if family == "" else "")
+
+    def keep(e: dict) -> bool:
+        if e["kernel_id"] == sibling:
+            return False
+        return e["kernel_id"] != kid or e["variant_id"] == variant
+
+    pack = filtered_pack(tmp_path / "pack", keep)
+    # Full and ragged tiles, N not a multiple of 4, depth not a multiple of 8
+    # (the element-wise loader) and of the 64-deep tile.
+    for m, k, n in ((512, 768, 3072), (17, 128, 40), (70, 72, 37), (300, 200, 264), (33, 100, 50), (1, 8, 4),
+                    (260, 96, 520)):
         g, feeds = gemm16_graph(rng, m, k, n, gelu, bias)
         out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
         ops = eng.ops()
@@ -250,6 +265,25 @@ def test_gemm_fp16_variants(tmp_path, variant, gelu, bias):
         want = oracle.evaluate(g, feeds)[g.outputs[0]]
         err = np.abs(out[g.outputs[0]].astype(np.float64) - want)
         assert err.max() <= 1e-2, f"{kid}:{variant} {(m, k, n)} max abs err {err.max():.3e}"
+
+
+def test_gemm_fp16_activation_operand_uses_b_as_is():
+    """With B an activation there is no transposed copy to read: only the
+    kernels that read B as it is lower, and they compute the product."""
+    rng = np.random.default_rng(31)
+    m, k, n = 96, 200, 72
+    g = workloads.GraphSpec()
+    g.inputs["a"] = ((m, k), "float16", "")
+    g.inputs["b"] = ((k, n), "float16", "")
+    g.add("gemm", "Gemm", ["a", "b"], ["y"])
+    g.outputs.append("y")
+    feeds = {"a": rng.standard_normal((m, k)).astype(np.float16),
+             "b": rng.normal(0, 0.05, (k, n)).astype(np.float16)}
+    out, eng, _ = run_graph(g, feeds)
+    candidates = eng.ops()[0].candidates
+    assert candidates and all(".fp16.mfma_kn:" in c for c in candidates), candidates
+    err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, feeds)["y"])
+    assert err.max() <= 1e-2, err.max()
 
 
 @pytest.mark.parametrize("rows,cols", [(512, 768), (17, 100), (4, 5000), (64, 1024)])
