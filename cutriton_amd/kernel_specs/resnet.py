@@ -34,8 +34,13 @@ CONV_TILES = (
     ("m64n128", 64, 128, 32),
     ("m128n64", 128, 64, 32),
     ("m64n64", 64, 64, 32),
+    ("m64n64k16", 64, 64, 16),
+    ("m64n128k16", 64, 128, 16),
+    ("m128n64k16", 128, 64, 16),
+    ("m64n64k64", 64, 64, 64),
+    ("m32n128", 32, 128, 32),
 )
-CONV_DEFAULT = "m128n128"
+CONV_DEFAULT = "m64n64"
 
 CONV_DIMENSIONS = (
     arg("n", "i32", "input_dim", index=0, axis=0),
@@ -82,6 +87,9 @@ SPLIT_TILES = (
     ("m128n128s2", 128, 128, 32, 2),
     ("m128n128s4", 128, 128, 32, 4),
     ("m128n128s8", 128, 128, 32, 8),
+    ("m64n64s2", 64, 64, 32, 2),
+    ("m64n64s4", 64, 64, 32, 4),
+    ("m64n64k64s2", 64, 64, 64, 2),
 )
 SPLIT_DEFAULT = "m128n128s4"
 SPLIT_SCRATCH_BYTES = 16384 * 4 + (128 << 20)
@@ -167,6 +175,10 @@ def register_gemm() -> None:
         {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
         {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
     )
+    # Split-K: z = SPLIT workgroups per output tile, runtime scratch as for
+    # the split-K convolutions.
+    split_tiles = (("m64n64s8", 64, 64, 32, 8), ("m64n64s16", 64, 64, 32, 16))
+    split_grid = grid + (meta("SPLIT"),)
     for kernel_id, prefix, inputs, extra in (
         ("gemm.fp32.mfma", "gemm_fp32", ("a", "b"), ()),
         ("gemm_bias.fp32.mfma", "gemm_bias_fp32", ("a", "b", "bias"),
@@ -182,6 +194,16 @@ def register_gemm() -> None:
         )
         register(KernelSpec(
             kernel_id, "Gemm", 1, CONV_SOURCE, arguments, grid, variants,
+            constraints=({"kind": "input_count_eq", "value": len(inputs)},) + common + extra,
+        ))
+        split_variants_ = tuple(
+            KernelVariant(name, f"{prefix}_{name}", num_warps=4,
+                          meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk, "SPLIT": split},
+                          default=name == "m64n64s8", scratch_bytes=SPLIT_SCRATCH_BYTES)
+            for name, bm, bn, bk, split in split_tiles
+        )
+        register(KernelSpec(
+            kernel_id.replace(".mfma", ".splitk"), "Gemm", 1, CONV_SOURCE, arguments, split_grid, split_variants_,
             constraints=({"kind": "input_count_eq", "value": len(inputs)},) + common + extra,
         ))
 

@@ -1,5 +1,5 @@
 // FP32 implicit-GEMM convolution family on CDNA4 FP32 MFMA
-// (v_mfma_f32_32x32x2_f32), with the BatchNorm / ReLU / residual-AddRelu
+// (v_mfma_f32_16x16x4_f32), with the BatchNorm / ReLU / residual-AddRelu
 // epilogue fused, plus the FP32 Gemm that shares the same core.
 //
 // Semantics follow the reference kernels in
@@ -21,9 +21,10 @@
 // Tiling. A workgroup (4 wavefronts) computes a BM x BN output tile and
 // walks the depth in BK-deep tiles, double buffered in LDS with the next
 // tile's global loads in flight during the MFMAs. The wavefronts form a
-// WGM x WGN x WGK grid: each owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA
+// WGM x WGN x WGK grid: each owns a (BM/WGM) x (BN/WGN) block of 16x16 MFMA
 // accumulators over 1/WGK of every depth tile; WGK > 1 partial sums are added
-// through LDS before the epilogue.
+// through LDS before the epilogue. The 16x16x4 form sustains a higher rate on
+// gfx950 than the 32x32x2 one.
 //
 // Split-K (SPLIT > 1): the grid carries SPLIT workgroups per output tile,
 // each accumulating an equal share of the depth tiles. Every share is written
@@ -37,16 +38,17 @@
 // only the shares travel through the coherent level.
 //
 // LDS holds both operands depth-contiguous, A as [m][d] and B as [j][d]
-// (rows padded by 4 floats), so one 16-byte read gives a lane four depths.
-// Within a depth tile the MFMA steps take the depths in the order
-//   step 4g + e, lane half h  ->  depth 8g + 4h + e
+// (rows padded by 4 floats, which keeps the 16 lanes of a read phase on
+// distinct banks), so one 16-byte read gives a lane four depths. A 16x16x4
+// MFMA takes depth slot q = lane / 16 from every lane; within a depth tile
+// the steps take the depths in the order
+//   step 4g + e, lane quarter q  ->  depth 16g + 4q + e
 // which visits every depth once; the sum is the same set of products.
 
 #include "common.h"
 
 namespace {
 
-using ct::f32x16;
 using ct::f32x4;
 
 enum Epilogue : int {
@@ -63,6 +65,10 @@ struct ConvGeometry {
 };
 
 constexpr int kThreads = 256;
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 // Raw buffer loads: an offset at or beyond the resource's byte range reads 0,
 // which is how zero padding and ragged tile edges are produced without
@@ -113,7 +119,7 @@ struct ConvLds {
   static constexpr int kA = BM * kRow;                     // one A buffer
   static constexpr int kB = BN * kRow;                     // one B buffer
   static constexpr int kTiles = 2 * (kA + kB);
-  static constexpr int kAccRegs = (BM / WGM / 32) * (BN / WGN / 32) * 16;
+  static constexpr int kAccRegs = (BM / WGM / 16) * (BN / WGN / 16) * 4;
   static constexpr int kReduce = (WGK - 1) * WGM * WGN * kAccRegs * 64;
   static constexpr int kEpi = 2 * BM;
   static constexpr int kFloats = (kTiles > kReduce ? kTiles : kReduce) + kEpi;
@@ -132,10 +138,10 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   using L = ConvLds<BM, BN, BK, WGM, WGN, WGK>;
   constexpr int WM = BM / WGM;
   constexpr int WN = BN / WGN;
-  constexpr int TM = WM / 32;
-  constexpr int TN = WN / 32;
+  constexpr int TM = WM / 16;
+  constexpr int TN = WN / 16;
   constexpr int ROW = L::kRow;
-  constexpr int GROUPS = BK / 8;                 // 8-depth groups per tile
+  constexpr int GROUPS = BK / 16;                // 16-depth groups per tile
   constexpr int WAVE_GROUPS = GROUPS / WGK;      // groups per wavefront
   constexpr int A_CHUNKS = BM * BK / 4 / kThreads;  // float4 chunks per thread
   constexpr int B_RUN = BK * BN / kThreads;         // depths per thread (one column)
@@ -327,35 +333,84 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     }
   };
 
-  f32x16 acc[TM][TN];
+  f32x4 acc[TM][TN];
 
   const int wk = wave / (WGM * WGN);
   const int wmn = wave % (WGM * WGN);
   const int wm = (wmn / WGN) * WM;
   const int wn = (wmn % WGN) * WN;
-  const int half = lane >> 5;
-  const int lane32 = lane & 31;
+  const int quarter = lane >> 4;
+  const int lane16 = lane & 15;
 
-  // MFMAs of one LDS depth tile (buffer `cur`) into acc.
+  // MFMAs of one LDS depth tile (buffer `cur`) into acc. The fragments of
+  // group g + 1 are read while the MFMAs of group g run; the scheduling
+  // groups at the end fix that order (first reads, then one LDS read after
+  // each of the first TM + TN MFMAs of a group).
   auto compute_tile = [&](int cur) {
-    const float* at = a_tile + cur * L::kA + (wm + lane32) * ROW + 4 * half;
-    const float* bt = b_tile + cur * L::kB + (wn + lane32) * ROW + 4 * half;
+    const float* at = a_tile + cur * L::kA + (wm + lane16) * ROW + 4 * quarter;
+    const float* bt = b_tile + cur * L::kB + (wn + lane16) * ROW + 4 * quarter;
+    f32x4 av[2][TM];
+    f32x4 bv[2][TN];
+    auto read_frags = [&](int gi, f32x4* fa, f32x4* fb) {
+      const int col = (wk * WAVE_GROUPS + gi) * 16;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const f32x4*>(at + i * 16 * ROW + col);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) fb[t] = *reinterpret_cast<const f32x4*>(bt + t * 16 * ROW + col);
+    };
+    read_frags(0, av[0], bv[0]);
 #pragma unroll
     for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
-      const int col = (wk * WAVE_GROUPS + gi) * 8;
-      f32x4 av[TM];
-      f32x4 bv[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const f32x4*>(at + i * 32 * ROW + col);
-#pragma unroll
-      for (int t = 0; t < TN; ++t) bv[t] = *reinterpret_cast<const f32x4*>(bt + t * 32 * ROW + col);
+      const int c = gi & 1;
+      if (gi + 1 < WAVE_GROUPS) read_frags(gi + 1, av[c ^ 1], bv[c ^ 1]);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int t = 0; t < TN; ++t)
-            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[t][e], acc[i][t], 0, 0, 0);
+            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][i][e], bv[c][t][e], acc[i][t], 0, 0, 0);
+    }
+    constexpr int READS = TM + TN;
+    constexpr int MFMAS = 4 * TM * TN;
+    constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS, 0);
+#pragma unroll
+    for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
+      if (gi + 1 < WAVE_GROUPS) {
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+        if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS, 0);
+      }
+    }
+  };
+
+  // Residual of the lane's outputs (residual-join epilogue without split-K):
+  // loaded before the last depth tile is multiplied, so its latency hides
+  // behind those MFMAs instead of stalling the epilogue.
+  constexpr bool PREFETCH_RESIDUAL = EPI == kBatchNormAddRelu && SPLIT == 1;
+  float res_pre[PREFETCH_RESIDUAL ? TM : 1][PREFETCH_RESIDUAL ? TN : 1][4];
+  auto prefetch_residual = [&]() {
+    if (!PREFETCH_RESIDUAL || wk != 0) return;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int col = n0 + wn + t * 16 + lane16;
+      const bool col_ok = col < columns;
+      const int cimg = col_ok ? col / pq : 0;
+      const size_t col_base = static_cast<size_t>(cimg) * g.k * pq + (col - cimg * pq);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm + i * 16 + 4 * quarter + r;
+          res_pre[PREFETCH_RESIDUAL ? i : 0][PREFETCH_RESIDUAL ? t : 0][r] =
+              (col_ok && row < g.k) ? residual[col_base + static_cast<size_t>(row) * pq] : 0.0f;
+        }
     }
   };
 
@@ -367,7 +422,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][t][r] = 0.0f;
+        for (int r = 0; r < 4; ++r) acc[i][t][r] = 0.0f;
     if (CHANNEL_RUN) seek_run(kb);
     load_tile(st0, kb * BK);
     store_tile(st0, 0);
@@ -376,39 +431,53 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
       const int cur = (kt - kb) & 1;
       const bool more = kt + 1 < ke;
       if (more) load_tile(st0, (kt + 1) * BK);
+      if (!more) prefetch_residual();
       compute_tile(cur);
       if (more) store_tile(st0, cur ^ 1);
       __syncthreads();
     }
   };
 
-  // Epilogue of the current tile. Lane holds column (lane % 32) of each
-  // 32x32 tile and rows 8*(r/4) + 4*(lane/32) + (r%4) for register r.
+  // Epilogue of the current tile. Lane holds column (lane % 16) of each
+  // 16x16 tile and rows 4*(lane/16) + r for register r: four consecutive
+  // output channels of one pixel.
   auto from_acc = [&](int i, int t, int r) { return acc[i][t][r]; };
   auto store_output = [&](auto value) {
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const int col = n0 + wn + t * 32 + lane32;
+      const int col = n0 + wn + t * 16 + lane16;
       if (col >= columns) continue;
       const int cimg = col / pq;
       const int cpix = col - cimg * pq;
       const size_t col_base = static_cast<size_t>(cimg) * g.k * pq + cpix;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
+        const int lrow0 = wm + i * 16 + 4 * quarter;
+        f32x4 mul = {1.0f, 1.0f, 1.0f, 1.0f}, add = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
+          // The four rows are consecutive channels: one 16-byte read each.
+          mul = *reinterpret_cast<const f32x4*>(epi_mul + lrow0);
+          add = *reinterpret_cast<const f32x4*>(epi_add + lrow0);
+        }
+        float res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (PREFETCH_RESIDUAL) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int lrow = wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int row = m0 + lrow;
+          for (int r = 0; r < 4; ++r) res[r] = res_pre[PREFETCH_RESIDUAL ? i : 0][PREFETCH_RESIDUAL ? t : 0][r];
+        } else if (EPI == kBatchNormAddRelu) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + lrow0 + r;
+            if (row < g.k) res[r] = residual[col_base + static_cast<size_t>(row) * pq];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + lrow0 + r;
           if (row >= g.k) continue;
           float v = value(i, t, r);
           const size_t at = col_base + static_cast<size_t>(row) * pq;
-          if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
-            // Rows r..r+3 of a group are consecutive channels: one 16-byte read.
-            const f32x4 mul = *reinterpret_cast<const f32x4*>(epi_mul + (lrow & ~3));
-            const f32x4 add = *reinterpret_cast<const f32x4*>(epi_add + (lrow & ~3));
-            v = fmaf(v, mul[r & 3], add[r & 3]);
-          }
-          if (EPI == kBatchNormAddRelu) v += residual[at];
+          if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v = fmaf(v, mul[r], add[r]);
+          if (EPI == kBatchNormAddRelu) v += res[r];
           if (EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v = fmaxf(v, 0.0f);
           if (EPI == kColumnBias) v += bias[col];
           output[at] = v;
@@ -443,14 +512,14 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
       unsigned* counters = static_cast<unsigned*>(scratch);
       float* shares = reinterpret_cast<float*>(static_cast<char*>(scratch) + kSplitCounterBytes) +
                       static_cast<size_t>(tile) * SPLIT * BM * BN;
-      constexpr int WAVE_REGS = TM * TN * 16 * 64;  // one wavefront's accumulators
+      constexpr int WAVE_REGS = TM * TN * 4 * 64;  // one wavefront's accumulators
       float* mine = shares + static_cast<size_t>(split) * BM * BN + wave * WAVE_REGS;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) StoreShared(mine + ((i * TN + t) * 16 + r) * 64 + lane, acc[i][t][r]);
+          for (int r = 0; r < 4; ++r) StoreShared(mine + ((i * TN + t) * 4 + r) * 64 + lane, acc[i][t][r]);
       // The shares must have reached the coherent level before the count.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -466,27 +535,27 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
       if (tid == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // Sum all shares in split order from the scratch (this workgroup's own
       // share is there too, stored and completed above).
-      // The 16 loads of one accumulator per share are issued together so
+      // The loads of one accumulator block per share are issued together so
       // that their latencies overlap.
       const float* base = shares + wave * WAVE_REGS + lane;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
-          const float* block = base + (i * TN + t) * 16 * 64;
-          float sum[16];
+          const float* block = base + (i * TN + t) * 4 * 64;
+          float sum[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sum[r] = LoadShared(block + r * 64);
+          for (int r = 0; r < 4; ++r) sum[r] = LoadShared(block + r * 64);
 #pragma unroll
           for (int sp = 1; sp < SPLIT; ++sp) {
-            float part[16];
+            float part[4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) part[r] = LoadShared(block + static_cast<size_t>(sp) * BM * BN + r * 64);
+            for (int r = 0; r < 4; ++r) part[r] = LoadShared(block + static_cast<size_t>(sp) * BM * BN + r * 64);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sum[r] += part[r];
+            for (int r = 0; r < 4; ++r) sum[r] += part[r];
           }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][t][r] = sum[r];
+          for (int r = 0; r < 4; ++r) acc[i][t][r] = sum[r];
         }
     }
   }
@@ -494,7 +563,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   // ---- Depth-split partial sums: wavefronts wk > 0 add theirs to wk == 0
   // through LDS (register r of lane l lands at [slot][r][l]).
   if (WGK > 1) {
-    constexpr int REGS = TM * TN * 16;
+    constexpr int REGS = TM * TN * 4;
     float* red = smem;
     if (wk > 0) {
       float* mine = red + ((wk - 1) * WGM * WGN + wmn) * REGS * 64;
@@ -503,7 +572,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
 #pragma unroll
         for (int t = 0; t < TN; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mine[((i * TN + t) * 16 + r) * 64 + lane] = acc[i][t][r];
+          for (int r = 0; r < 4; ++r) mine[((i * TN + t) * 4 + r) * 64 + lane] = acc[i][t][r];
     }
     __syncthreads();
     if (wk > 0) return;
@@ -515,7 +584,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
 #pragma unroll
         for (int t = 0; t < TN; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][t][r] += theirs[((i * TN + t) * 16 + r) * 64 + lane];
+          for (int r = 0; r < 4; ++r) acc[i][t][r] += theirs[((i * TN + t) * 4 + r) * 64 + lane];
     }
   }
 
@@ -584,7 +653,12 @@ CT_DEFINE_CONV_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
 CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1)
 CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2)
 CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2)
-CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
+CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m32n128, 32, 128, 32, 1, 4, 1)
 
 // Split-K entry points: the first reserved argument is the runtime scratch
 // (kSplitCounterBytes + kSplitShareBytes, zero-initialised by the engine).
@@ -629,6 +703,9 @@ CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
 CT_DEFINE_SPLIT_VARIANTS(m128n128s2, 128, 128, 32, 2, 2, 2)
 CT_DEFINE_SPLIT_VARIANTS(m128n128s4, 128, 128, 32, 2, 2, 4)
 CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s2, 64, 64, 32, 2, 2, 2)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s4, 64, 64, 32, 2, 2, 4)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one
@@ -660,5 +737,42 @@ CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8)
     }                                                                                                     \
   }
 
-CT_DEFINE_GEMM_VARIANTS(m64n64, 64, 64, 32, 1, 1, 4)
+CT_DEFINE_GEMM_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1)
 CT_DEFINE_GEMM_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
+
+// Split-K Gemm entry points (grid z = SPLIT; the first reserved argument is
+// the runtime scratch, as for the split-K convolutions): a short, wide
+// product such as the classifier [N, 2048] x [2048, 1000] has few output
+// tiles, so the depth is shared out to fill the chip.
+#define CT_DEFINE_GEMM_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT)                                  \
+  CT_KERNEL void __launch_bounds__(kThreads) gemm_fp32_##NAME(const float* a, const float* b, float* output, \
+                                                              int m, int n, int k, void* scratch, void*) { \
+    __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, 1>::kFloats];        \
+    const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
+    if (k % BK == 0) {                                                                                    \
+      ConvCore<BM, BN, BK, WGM, WGN, 1, kPlain, false, SPLIT, true>(smem, b, a, nullptr, nullptr, nullptr, \
+                                                                       nullptr, nullptr, output, g, 0.0f, \
+                                                                       scratch);                          \
+    } else {                                                                                              \
+      ConvCore<BM, BN, BK, WGM, WGN, 1, kPlain, true, SPLIT>(smem, b, a, nullptr, nullptr, nullptr,       \
+                                                             nullptr, nullptr, output, g, 0.0f, scratch); \
+    }                                                                                                     \
+  }                                                                                                       \
+  CT_KERNEL void __launch_bounds__(kThreads) gemm_bias_fp32_##NAME(                                      \
+      const float* a, const float* b, const float* bias, float* output, int m, int n, int k, void* scratch, \
+      void*) {                                                                                            \
+    __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, 1>::kFloats];        \
+    const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
+    if (k % BK == 0) {                                                                                    \
+      ConvCore<BM, BN, BK, WGM, WGN, 1, kColumnBias, false, SPLIT, true>(smem, b, a, nullptr, bias,      \
+                                                                            nullptr, nullptr, nullptr,    \
+                                                                            output, g, 0.0f, scratch);    \
+    } else {                                                                                              \
+      ConvCore<BM, BN, BK, WGM, WGN, 1, kColumnBias, true, SPLIT>(smem, b, a, nullptr, bias, nullptr,    \
+                                                                  nullptr, nullptr, output, g, 0.0f,      \
+                                                                  scratch);                               \
+    }                                                                                                     \
+  }
+
+CT_DEFINE_GEMM_SPLIT_VARIANTS(m64n64s8, 64, 64, 32, 2, 2, 8)
+CT_DEFINE_GEMM_SPLIT_VARIANTS(m64n64s16, 64, 64, 32, 2, 2, 16)

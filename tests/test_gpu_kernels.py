@@ -20,7 +20,9 @@ from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant
 pytestmark = pytest.mark.gpu
 
 CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
+                 "mfma:m64n64k16", "mfma:m64n128k16", "mfma:m128n64k16", "mfma:m64n64k64", "mfma:m32n128",
                  "splitk:m128n128s2", "splitk:m128n128s4", "splitk:m128n128s8",
+                 "splitk:m64n64s2", "splitk:m64n64s4", "splitk:m64n64k64s2",
                  "direct:d64n256", "direct:d64n64", "direct:d32n64")
 # (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
 # "_kn" reads B as it is.
@@ -96,7 +98,7 @@ def test_conv_family_variants(tmp_path, family_variant, tail, kernel_base):
         assert_close_fp32(out[g.outputs[0]], want, what=f"{kernel_id}:{variant} {shape}")
 
 
-@pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8"])
+@pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8", "m64n64s4"])
 def test_split_k_shares_follow_the_inputs(tmp_path, variant):
     """Split-K partial sums travel through the runtime scratch and the tile
     counters reset themselves: consecutive launches on one context with
@@ -175,13 +177,20 @@ def test_tuner_runs_every_candidate(tmp_path):
     assert np.array_equal(out[g.outputs[0]], out2[g.outputs[0]])
 
 
-@pytest.mark.parametrize("variant", ("m64n64", "m128n128"))
+@pytest.mark.parametrize("family,variant", (("mfma", "m64n64"), ("mfma", "m128n128"), ("splitk", "m64n64s8"),
+                                            ("splitk", "m64n64s16")))
 @pytest.mark.parametrize("m,k,n,bias", [(32, 2048, 1000, False), (5, 37, 29, True), (130, 64, 70, False),
                                          (3, 2048, 1000, True)])
-def test_gemm_fp32(tmp_path, variant, m, k, n, bias):
+def test_gemm_fp32(tmp_path, family, variant, m, k, n, bias):
     rng = np.random.default_rng(3)
-    kid = "gemm_bias.fp32.mfma" if bias else "gemm.fp32.mfma"
-    pack = filtered_pack(tmp_path / "pack", only_variant(kid, variant))
+    base = "gemm_bias.fp32" if bias else "gemm.fp32"
+    kid = f"{base}.{family}"
+    sibling = f"{base}.{'splitk' if family == 'mfma' else 'mfma'}"
+
+    def keep(e: dict) -> bool:
+        return e["kernel_id"] != sibling and (e["kernel_id"] != kid or e["variant_id"] == variant)
+
+    pack = filtered_pack(tmp_path / "pack", keep)
     g = workloads.GraphSpec()
     g.inputs["a"] = ((m, k), "float32", "")
     g.constant("b", rng.normal(0, 0.05, (k, n)).astype(np.float32))
