@@ -65,6 +65,10 @@ GEMM_NT_TILES = (
     ("m128n128k128w4", 128, 128, 128, 4),
     ("m64n128w4", 64, 128, 64, 4),
     ("m64n64w4", 64, 64, 64, 4),
+    ("m256n128w8", 256, 128, 64, 8),
+    ("m128n256w8", 128, 256, 64, 8),
+    ("m128n128w8", 128, 128, 64, 8),
+    ("m128n128k128w8", 128, 128, 128, 8),
 )
 GEMM_NT_DEFAULT = "m128n128w4"
 

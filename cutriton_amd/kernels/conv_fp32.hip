@@ -64,8 +64,6 @@ struct ConvGeometry {
   int stride_h, stride_w, pad_h, pad_w, dil_h, dil_w;
 };
 
-constexpr int kThreads = 256;
-
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
@@ -143,12 +141,12 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   constexpr int ROW = L::kRow;
   constexpr int GROUPS = BK / 16;                // 16-depth groups per tile
   constexpr int WAVE_GROUPS = GROUPS / WGK;      // groups per wavefront
-  constexpr int A_CHUNKS = BM * BK / 4 / kThreads;  // float4 chunks per thread
-  constexpr int B_RUN = BK * BN / kThreads;         // depths per thread (one column)
-  static_assert(WGM * WGN * WGK == kThreads / 64, "four wavefronts per workgroup");
+  constexpr int THREADS = 64 * WGM * WGN * WGK;     // one wavefront per wave-grid cell
+  constexpr int A_CHUNKS = BM * BK / 4 / THREADS;   // float4 chunks per thread
+  constexpr int B_RUN = BK * BN / THREADS;          // depths per thread (one column)
   static_assert(TM >= 1 && TN >= 1 && WAVE_GROUPS >= 1, "wave tile too small");
-  static_assert(A_CHUNKS >= 1 && A_CHUNKS * kThreads * 4 == BM * BK, "A tile split");
-  static_assert(kThreads % BN == 0 && B_RUN % 4 == 0, "B tile split");
+  static_assert(A_CHUNKS >= 1 && A_CHUNKS * THREADS * 4 == BM * BK, "A tile split");
+  static_assert(THREADS % BN == 0 && B_RUN % 4 == 0, "B tile split");
   static_assert(SPLIT == 1 || WGK == 1, "split-K variants keep the depth whole inside a workgroup");
 
   float* a_tile = smem;                  // [2][BM][ROW]
@@ -195,7 +193,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     m0 = (t % tiles_m) * BM;
     n0 = (t / tiles_m) * BN;
     if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
-      for (int i = tid; i < BM; i += kThreads) {
+      for (int i = tid; i < BM; i += THREADS) {
         const int m = m0 + i;
         const bool ok = m < g.k;
         const float mul = ok ? scale[m] * rsqrtf(variance[m] + epsilon) : 0.0f;
@@ -242,7 +240,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     const int tap = run_r * g.s + run_s;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int chunk = tid + kThreads * i;
+      const int chunk = tid + THREADS * i;
       const int m = m0 + chunk / (BK / 4);
       const int c = run_c0 + (chunk % (BK / 4)) * 4;
       // OHWI weight: the channels of one tap are contiguous.
@@ -274,7 +272,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     float* rb = st.b;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int chunk = tid + kThreads * i;
+      const int chunk = tid + THREADS * i;
       const int m = m0 + chunk / (BK / 4);
       const int d = d0 + (chunk % (BK / 4)) * 4;
       const int base = m * depth + d;
@@ -323,7 +321,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     float* bt = b_tile + buf * L::kB;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int chunk = tid + kThreads * i;
+      const int chunk = tid + THREADS * i;
       *reinterpret_cast<f32x4*>(at + (chunk / (BK / 4)) * ROW + (chunk % (BK / 4)) * 4) = ra[i];
     }
 #pragma unroll
@@ -623,27 +621,28 @@ __device__ __forceinline__ ConvGeometry MakeGeometry(int n, int c, int h, int w,
   }
 
 #define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_relu_fp32_##NAME(                                  \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_relu_fp32_##NAME(                     \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormRelu, x, weight, scale, bias, mean, variance,      \
                 nullptr, output, CT_CONV_GEOMETRY, epsilon)                                              \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_fp32_##NAME(                                       \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_fp32_##NAME(                          \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNorm, x, weight, scale, bias, mean, variance, nullptr, \
                 output, CT_CONV_GEOMETRY, epsilon)                                                       \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_add_relu_fp32_##NAME(                              \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_add_relu_fp32_##NAME(                 \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon, void*,   \
       void*) {                                                                                           \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormAddRelu, x, weight, scale, bias, mean, variance,   \
                 residual, output, CT_CONV_GEOMETRY, epsilon)                                             \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_fp32_##NAME(const float* x, const float* weight,      \
-                                                              float* output, CT_CONV_DIMS, void*, void*) { \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_fp32_##NAME(const float* x,                \
+                                                              const float* weight, float* output,        \
+                                                              CT_CONV_DIMS, void*, void*) {              \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr,       \
                 nullptr, output, CT_CONV_GEOMETRY, 0.0f)                                                 \
   }
@@ -673,26 +672,26 @@ CT_DEFINE_CONV_VARIANTS(m32n128, 32, 128, 32, 1, 4, 1)
   }
 
 #define CT_DEFINE_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT)                                   \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_relu_fp32_##NAME(                                  \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_relu_fp32_##NAME(                                  \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormRelu, x, weight, scale, bias, mean,         \
                       variance, nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                     \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_fp32_##NAME(                                       \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_fp32_##NAME(                                       \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNorm, x, weight, scale, bias, mean, variance,   \
                       nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                               \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_bn_add_relu_fp32_##NAME(                              \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_add_relu_fp32_##NAME(                              \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon,          \
       void* scratch, void*) {                                                                            \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormAddRelu, x, weight, scale, bias, mean,      \
                       variance, residual, output, CT_CONV_GEOMETRY, epsilon, scratch)                    \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(kThreads) conv_fp32_##NAME(const float* x, const float* weight,      \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_fp32_##NAME(const float* x, const float* weight,      \
                                                               float* output, CT_CONV_DIMS, void* scratch, \
                                                               void*) {                                   \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr, \
@@ -711,8 +710,8 @@ CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one
 // 1 x n "image").
 #define CT_DEFINE_GEMM_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                           \
-  CT_KERNEL void __launch_bounds__(kThreads) gemm_fp32_##NAME(const float* a, const float* b, float* output, \
-                                                              int m, int n, int k, void*, void*) {        \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) gemm_fp32_##NAME(const float* a, const float* b, \
+                                                              float* output, int m, int n, int k, void*, void*) {        \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
     if (k % BK == 0) {                                                                                    \
@@ -723,7 +722,7 @@ CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
                                                         nullptr, output, g, 0.0f);                        \
     }                                                                                                     \
   }                                                                                                       \
-  CT_KERNEL void __launch_bounds__(kThreads) gemm_bias_fp32_##NAME(                                      \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) gemm_bias_fp32_##NAME(                         \
       const float* a, const float* b, const float* bias, float* output, int m, int n, int k, void*, void*) { \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, WGK>::kFloats];      \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
@@ -745,7 +744,7 @@ CT_DEFINE_GEMM_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
 // product such as the classifier [N, 2048] x [2048, 1000] has few output
 // tiles, so the depth is shared out to fill the chip.
 #define CT_DEFINE_GEMM_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT)                                  \
-  CT_KERNEL void __launch_bounds__(kThreads) gemm_fp32_##NAME(const float* a, const float* b, float* output, \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) gemm_fp32_##NAME(const float* a, const float* b, float* output, \
                                                               int m, int n, int k, void* scratch, void*) { \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, 1>::kFloats];        \
     const ConvGeometry g = MakeGeometry(1, k, 1, n, m, 1, 1, 1, n, 1, 1, 0, 0, 1, 1);                    \
@@ -758,7 +757,7 @@ CT_DEFINE_GEMM_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
                                                              nullptr, nullptr, output, g, 0.0f, scratch); \
     }                                                                                                     \
   }                                                                                                       \
-  CT_KERNEL void __launch_bounds__(kThreads) gemm_bias_fp32_##NAME(                                      \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) gemm_bias_fp32_##NAME(                                      \
       const float* a, const float* b, const float* bias, float* output, int m, int n, int k, void* scratch, \
       void*) {                                                                                            \
     __shared__ __attribute__((aligned(16))) float smem[ConvLds<BM, BN, BK, WGM, WGN, 1>::kFloats];        \

@@ -359,3 +359,7 @@ CT_DEFINE_GEMM_NT(m128n128w4, 128, 128, 64, 2, 2, 2)
 CT_DEFINE_GEMM_NT(m128n128k128w4, 128, 128, 128, 2, 2, 2)
 CT_DEFINE_GEMM_NT(m64n128w4, 64, 128, 64, 2, 1, 4)
 CT_DEFINE_GEMM_NT(m64n64w4, 64, 64, 64, 2, 2, 2)
+CT_DEFINE_GEMM_NT(m256n128w8, 256, 128, 64, 2, 4, 2)
+CT_DEFINE_GEMM_NT(m128n256w8, 128, 256, 64, 2, 2, 4)
+CT_DEFINE_GEMM_NT(m128n128w8, 128, 128, 64, 2, 2, 4)
+CT_DEFINE_GEMM_NT(m128n128k128w8, 128, 128, 128, 2, 2, 4)

@@ -27,7 +27,8 @@ CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64"
 # (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
 # "_kn" reads B as it is.
 GEMM16_VARIANTS = tuple(("", v) for v in ("m256n256w4", "m256n256w8", "m256n128w4", "m128n256w4", "m128n128w4",
-                                          "m128n128k128w4", "m64n128w4", "m64n64w4")) + \
+                                          "m128n128k128w4", "m64n128w4", "m64n64w4", "m256n128w8", "m128n256w8",
+                                          "m128n128w8", "m128n128k128w8")) + \
     tuple(("_kn", v) for v in ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64"))
 
 
@@ -274,6 +275,45 @@ def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
         want = oracle.evaluate(g, feeds)[g.outputs[0]]
         err = np.abs(out[g.outputs[0]].astype(np.float64) - want)
         assert err.max() <= 1e-2, f"{kid}:{variant} {(m, k, n)} max abs err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("family", ["", "_kn"])
+def test_gemm_gelu_epilogue_over_the_activation_range(tmp_path, family):
+    """The fused erf-GELU epilogue on exactly known pre-activations: a one-hot
+    product passes a[i, 0] + bias[j] through unchanged, for a[i, 0] over
+    [-12, 12] and the special values 0 and +-1e-6, so each output is within
+    one FP16 rounding (plus the erfc evaluation's 1e-6) of GELU(a + bias)
+    evaluated in float64."""
+    from scipy.special import erf
+
+    m, k, n = 520, 16, 64
+    vals = np.concatenate([np.linspace(-12.0, 12.0, m - 8), [0.0, 1e-6, -1e-6, 0.5, -0.5, 3.0, -3.0, 8.0]])
+    a = np.zeros((m, k), np.float16)
+    a[:, 0] = vals.astype(np.float16)
+    b = np.zeros((k, n), np.float16)
+    b[0, :] = 1.0
+    bias = np.zeros(n, np.float16)
+    bias[n // 2:] = np.linspace(-0.25, 0.25, n - n // 2).astype(np.float16)
+    g = workloads.GraphSpec()
+    g.inputs["a"] = ((m, k), "float16", "")
+    g.constant("b", b)
+    g.constant("bias", bias)
+    y = g.add("gemm", "Gemm", ["a", "b", "bias"], ["h"])
+    g.add("gelu", "Gelu", [y], ["y"])
+    g.outputs.append("y")
+    base = "gemm_gelu_bias.fp16.mfma"
+    kid, sibling = base + family, base + ("_kn" if family == "" else "")
+    pack = filtered_pack(tmp_path / "pack", lambda e: e["kernel_id"] != sibling)
+    out, eng, _ = run_graph(g, {"a": a}, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    assert kid + ":" in eng.ops()[0].candidates[eng.ops()[0].selected_candidate]
+    pre = a[:, :1].astype(np.float64) + bias[None, :].astype(np.float64)
+    want = 0.5 * pre * (1.0 + erf(pre / np.sqrt(2.0)))
+    # One FP16 rounding (2^-11 relative, doubled) plus the absolute error of
+    # the FP32 erfc evaluation (below 1e-6, doubled): the floor matters only
+    # in the negative tail, where GELU is a few 1e-6.
+    err = np.abs(out["y"].astype(np.float64) - want)
+    bound = 2.0 ** -10 * np.abs(want) + 2e-6
+    assert np.all(err <= bound), (err.max(), pre.ravel()[np.argmax(err - bound)])
 
 
 def test_gemm_fp16_activation_operand_uses_b_as_is():
