@@ -122,6 +122,18 @@ bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const Val
         }
         break;
       }
+      case KernelConstraintKind::kTensorDimAtMost: {
+        const auto& names = c.tensor_is_output ? node.outputs() : node.inputs();
+        if (c.tensor_index < 0 || static_cast<std::size_t>(c.tensor_index) >= names.size()) {
+          return false;
+        }
+        const ValueDesc* v = lookup(names[static_cast<std::size_t>(c.tensor_index)]);
+        if (v == nullptr || static_cast<std::size_t>(c.tensor_axis) >= v->tensor.shape.size() ||
+            v->tensor.shape[static_cast<std::size_t>(c.tensor_axis)] > c.expected) {
+          return false;
+        }
+        break;
+      }
     }
   }
   return true;

@@ -158,14 +158,18 @@ KernelConstraint ParseConstraint(const Value& v) {
     c.default_value = IntOr(v, "default", 0);
   } else if (kind == "input_count_eq") {
     c.kind = KernelConstraintKind::kInputCountEquals;
-  } else if (kind == "tensor_rank_eq") {
-    c.kind = KernelConstraintKind::kTensorRankEquals;
+  } else if (kind == "tensor_rank_eq" || kind == "dim_le") {
+    c.kind = kind == "dim_le" ? KernelConstraintKind::kTensorDimAtMost : KernelConstraintKind::kTensorRankEquals;
     const std::string source = v.at("source").string();
     if (source != "input" && source != "output") {
-      throw std::runtime_error("tensor_rank_eq source must be input or output");
+      throw std::runtime_error(kind + " source must be input or output");
     }
     c.tensor_is_output = source == "output";
     c.tensor_index = IntOr(v, "index", 0);
+    if (kind == "dim_le") {
+      c.tensor_axis = static_cast<int>(AsInt(v.at("axis")));
+      if (c.tensor_axis < 0) throw std::runtime_error("dim_le axis must be non-negative");
+    }
   } else {
     throw std::runtime_error("unsupported kernel constraint: " + kind);
   }

@@ -53,6 +53,8 @@ CONSTRAINTS: dict[str, frozenset[str]] = {
     "attribute_i64_eq": frozenset({"kind", "name", "value", "default"}),
     "input_count_eq": frozenset({"kind", "value"}),
     "tensor_rank_eq": frozenset({"kind", "source", "index", "value"}),
+    # shape[axis] of an input/output is at most value
+    "dim_le": frozenset({"kind", "source", "index", "axis", "value"}),
 }
 
 ARGUMENT_TYPES = frozenset({"*fp32", "*fp16", "*i8", "i32", "fp32"})
@@ -139,8 +141,10 @@ class KernelSpec:
             kind = constraint.get("kind")
             if kind not in CONSTRAINTS or set(constraint) - CONSTRAINTS[kind]:
                 raise ValueError(f"{self.kernel_id}: unsafe constraint")
-            if kind == "tensor_rank_eq" and constraint.get("source") not in {"input", "output"}:
+            if kind in {"tensor_rank_eq", "dim_le"} and constraint.get("source") not in {"input", "output"}:
                 raise ValueError(f"{self.kernel_id}: invalid tensor constraint source")
+            if kind == "dim_le" and (not isinstance(constraint.get("axis"), int) or constraint["axis"] < 0):
+                raise ValueError(f"{self.kernel_id}: dim_le needs a non-negative axis")
 
 
 def _validate_grid(kernel_id: str, grid: Any, variants: tuple[KernelVariant, ...]) -> None:

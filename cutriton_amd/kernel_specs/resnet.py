@@ -123,6 +123,23 @@ def direct_variants(prefix: str) -> tuple[KernelVariant, ...]:
     )
 
 
+# Few-channel variant (conv_small_c_fp32.hip): C <= 4 and kernels up to 7x7
+# (the stem). x: images * ceil(P / 2) * ceil(Q / 112), y: ceil(K / 64).
+SMALLC_SOURCE = "conv_small_c_fp32.hip"
+SMALLC_GRID = (
+    mul(mul(output_dim(0), ceil_div(output_dim(2), literal(2))), ceil_div(output_dim(3), literal(112))),
+    ceil_div(output_dim(1), literal(64)),
+)
+SMALLC_CONSTRAINTS = tuple(
+    {"kind": "dim_le", "source": "input", "index": 1, "axis": axis, "value": bound}
+    for axis, bound in ((1, 4), (2, 7), (3, 7))
+)
+
+
+def smallc_variants(prefix: str) -> tuple[KernelVariant, ...]:
+    return (KernelVariant("r2c64", f"{prefix}_smallc", num_warps=4, default=True),)
+
+
 def register_conv_family() -> None:
     # conv_fp32.hip reads the weight as OHWI (a channel run of one tap is
     # contiguous); conv_direct_fp32.hip reads OIHW.
@@ -132,23 +149,24 @@ def register_conv_family() -> None:
             for i, name in enumerate(("x", "weight", "scale", "bias", "mean", "variance"))
         )
     epsilon = arg("epsilon", "fp32", "attribute_f64", name="batchnorm_epsilon", default=1e-5)
-    families = ((CONV_SOURCE, "mfma", conv_variants, CONV_GRID, "OHWI"),
-                (CONV_SOURCE, "splitk", split_variants, SPLIT_GRID, "OHWI"),
-                (DIRECT_SOURCE, "direct", direct_variants, CONV_GRID, None))
+    families = ((CONV_SOURCE, "mfma", conv_variants, CONV_GRID, "OHWI", ()),
+                (CONV_SOURCE, "splitk", split_variants, SPLIT_GRID, "OHWI", ()),
+                (DIRECT_SOURCE, "direct", direct_variants, CONV_GRID, None, ()),
+                (SMALLC_SOURCE, "smallc", smallc_variants, SMALLC_GRID, None, SMALLC_CONSTRAINTS))
     residual = (arg("residual", "*fp32", "input", index=6),)
     for op_type, kernel_id, prefix, extra in (
         ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw", "conv_bn_relu_fp32", ()),
         ("FusedConvBatchNorm", "conv_bn.fp32.nchw", "conv_bn_fp32", ()),
         ("FusedConvBatchNormAddRelu", "conv_bn_add_relu.fp32.nchw", "conv_bn_add_relu_fp32", residual),
     ):
-        for source, suffix, variants, grid, weight_layout in families:
+        for source, suffix, variants, grid, weight_layout, more in families:
             inputs = bn_inputs_for(weight_layout) + extra
             arguments = inputs + (arg("output", "*fp32", "output", index=0),) + CONV_DIMENSIONS + (epsilon,) + reserved()
             register(KernelSpec(
                 f"{kernel_id}.{suffix}", op_type, 1, source, arguments, grid, variants(prefix),
-                layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},),
+                layout="NCHW", constraints=({"kind": "input_count_eq", "value": len(inputs)},) + more,
             ))
-    for source, suffix, variants, grid, weight_layout in families:
+    for source, suffix, variants, grid, weight_layout, more in families:
         conv_arguments = (
             arg("x", "*fp32", "input", index=0),
             arg("weight", "*fp32", "input", index=1, **({"layout": weight_layout} if weight_layout else {})),
@@ -156,7 +174,7 @@ def register_conv_family() -> None:
         ) + CONV_DIMENSIONS + reserved()
         register(KernelSpec(
             f"conv.fp32.nchw.{suffix}", "Conv", 1, source, conv_arguments, grid, variants("conv_fp32"),
-            layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},),
+            layout="NCHW", constraints=({"kind": "input_count_eq", "value": 2},) + more,
         ))
 
 

@@ -69,6 +69,7 @@ enum class KernelConstraintKind {
   kAttributeInt64Equals,
   kInputCountEquals,
   kTensorRankEquals,
+  kTensorDimAtMost,  // "dim_le": shape[axis] of an input/output <= value
 };
 
 // Declarative constraint; packs cannot inject code.
@@ -77,6 +78,7 @@ struct KernelConstraint {
   std::string attribute_name;
   bool tensor_is_output{false};
   int tensor_index{0};
+  int tensor_axis{0};
   int64_t expected{0};
   int64_t default_value{0};
 };

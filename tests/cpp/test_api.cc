@@ -458,6 +458,28 @@ void KernelPackAbi() {
   EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
   write(with_source(y_source, R"("source": {"kind": "output", "index": 0, "layout": "OHWI"})"));
   EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
+  write(with_source(x_source, R"("source": {"kind": "input", "index": 0, "layout": "NK"})"));
+  EXPECT_OK(repo.Load({root.string()}));
+  if (!repo.artifacts().empty()) EXPECT(repo.artifacts().front().arguments[0].source.layout == "NK");
+
+  // dim_le constraints: parsed with their axis; a bad source or a missing
+  // axis is rejected.
+  auto with_constraints = [&](const std::string& list) {
+    std::string text = PackText(2, v2_grid);
+    const std::string from = "\"constraints\": []";
+    text.replace(text.find(from), from.size(), "\"constraints\": " + list);
+    return text;
+  };
+  write(with_constraints(R"([{"kind": "dim_le", "source": "input", "index": 0, "axis": 1, "value": 4}])"));
+  EXPECT_OK(repo.Load({root.string()}));
+  if (!repo.artifacts().empty() && !repo.artifacts().front().constraints.empty()) {
+    const KernelConstraint& c = repo.artifacts().front().constraints.front();
+    EXPECT(c.kind == KernelConstraintKind::kTensorDimAtMost && c.tensor_axis == 1 && c.expected == 4);
+  }
+  write(with_constraints(R"([{"kind": "dim_le", "source": "weights", "index": 0, "axis": 1, "value": 4}])"));
+  EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
+  write(with_constraints(R"([{"kind": "dim_le", "source": "input", "index": 0, "value": 4}])"));
+  EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
 
   // Too deep a grid tree (depth 9).
   std::string deep = R"({"kind":"literal","value":1})";

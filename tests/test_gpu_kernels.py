@@ -99,6 +99,42 @@ def test_conv_family_variants(tmp_path, family_variant, tail, kernel_base):
         assert_close_fp32(out[g.outputs[0]], want, what=f"{kernel_id}:{variant} {shape}")
 
 
+SMALLC_SHAPES = [
+    # n, c, h, w, k, r, stride, pad, dil
+    (2, 3, 31, 29, 16, 7, 2, 3, 1),     # stem-like, ragged rows and columns
+    (1, 3, 64, 240, 64, 7, 2, 3, 1),    # Q = 120: two column chunks
+    (2, 4, 9, 11, 40, 3, 1, 1, 1),      # 3x3, K = 40: a partial channel block
+    (1, 1, 12, 12, 8, 1, 1, 0, 1),      # 1x1, one channel
+    (1, 4, 40, 60, 8, 7, 1, 3, 6),      # dilation 6: the patch exceeds LDS (global path)
+]
+
+
+@pytest.mark.parametrize("tail,kernel_base", [
+    ("relu", "conv_bn_relu.fp32.nchw"),
+    ("bn", "conv_bn.fp32.nchw"),
+    ("add_relu", "conv_bn_add_relu.fp32.nchw"),
+    ("conv", "conv.fp32.nchw"),
+])
+def test_small_channel_conv(tmp_path, tail, kernel_base):
+    rng = np.random.default_rng(41)
+    kernel_id = f"{kernel_base}.smallc"
+    pack = filtered_pack(tmp_path / "pack", only_kernel_variant(kernel_id, "r2c64", kernel_base))
+    for shape in SMALLC_SHAPES:
+        g, feeds = conv_graph(rng, *shape, tail=tail)
+        out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+        ops = eng.ops()
+        assert len(ops) == 1 and ops[0].candidates[ops[0].selected_candidate].endswith(f"{kernel_id}:r2c64"), ops
+        assert_close_fp32(out[g.outputs[0]], oracle.evaluate(g, feeds)[g.outputs[0]], what=f"{kernel_id} {shape}")
+
+
+def test_small_channel_conv_does_not_match_wide_inputs():
+    """dim_le keeps the few-channel kernel off a convolution with C = 8."""
+    rng = np.random.default_rng(43)
+    g, _ = conv_graph(rng, 1, 8, 12, 12, 16, 3, 1, 1, 1, tail="relu")
+    ops = engine.build_engine(workloads.to_model(g), engine.CompileOptions(tuning_mode="disabled")).ops()
+    assert not any(".smallc:" in cand for cand in ops[0].candidates), ops[0].candidates
+
+
 @pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8", "m64n64s4"])
 def test_split_k_shares_follow_the_inputs(tmp_path, variant):
     """Split-K partial sums travel through the runtime scratch and the tile

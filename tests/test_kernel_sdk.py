@@ -97,6 +97,23 @@ def test_rejects_arbitrary_grid_and_constraint_expressions():
         _spec(constraints=({"kind": "python", "expression": "x"},)).validate()
 
 
+def test_dim_le_constraint_is_checked():
+    ok = {"kind": "dim_le", "source": "input", "index": 1, "axis": 1, "value": 4}
+    _spec(constraints=(ok,)).validate()
+    with pytest.raises(ValueError, match="source"):
+        _spec(constraints=({**ok, "source": "attribute"},)).validate()
+    with pytest.raises(ValueError, match="axis"):
+        _spec(constraints=({**ok, "axis": -1},)).validate()
+    with pytest.raises(ValueError, match="unsafe constraint"):
+        _spec(constraints=({**ok, "expression": "x"},)).validate()
+
+
+def test_input_layout_nk_is_accepted():
+    spec = _spec()
+    laid_out = (ArgumentSpec("x", "*fp32", {"kind": "input", "index": 0, "layout": "NK"}),) + spec.arguments[1:]
+    _spec(arguments=laid_out).validate()
+
+
 def test_accepts_safe_multidimensional_grid():
     _spec(
         variants=(KernelVariant("tiled", "relu_fp32", meta={"BLOCK": 64}, default=True),),
