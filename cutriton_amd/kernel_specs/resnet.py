@@ -281,7 +281,9 @@ def register_bandwidth_kernels() -> None:
         arg("dilation_w", "i32", "attribute_i64", name="dilations", index=1, default=1),
     ) + reserved()
     register(KernelSpec(
-        "max_pool.fp32.nchw", "MaxPool", 1, "pool_fp32.hip", pool_arguments, numel_grid(256),
+        "max_pool.fp32.nchw", "MaxPool", 1, "pool_fp32.hip", pool_arguments,
+        # One workgroup per (image, channel) plane and band of 8 output rows.
+        (mul(mul(output_dim(0), output_dim(1)), ceil_div(output_dim(2), literal(8))),),
         variants("max_pool_fp32_nchw"), layout="NCHW",
     ))
 

@@ -15,32 +15,77 @@ constexpr int kThreads = 256;
 
 }  // namespace
 
-// One thread per output element, in output order: neighbouring lanes take
-// neighbouring output columns, so each window row is a short strided run that
-// the wave reads from a few cache lines.
+// A workgroup takes one (image, channel) plane and a band of kBand output
+// rows. The input rows the band's windows read are copied once into LDS (one
+// contiguous span, 16 bytes per lane), rows outside the image as -inf; each
+// output is then the max over its window read from LDS, kernel row outer,
+// kernel column inner, skipping columns outside the image. Grid:
+// planes * ceil(out_h / kBand). A band too tall for LDS (large strides or
+// dilations) reads its windows from global memory instead.
+namespace {
+constexpr int kBand = 8;
+constexpr int kPoolLds = 4096;  // floats
+}  // namespace
+
 CT_KERNEL void __launch_bounds__(kThreads)
     max_pool_fp32_nchw(const float* __restrict__ x, float* __restrict__ output, int n, int c, int h, int w,
                        int out_h, int out_w, int kernel_h, int kernel_w, int stride_h, int stride_w, int pad_h,
                        int pad_w, int dilation_h, int dilation_w, void*, void*) {
-  const int64_t total = static_cast<int64_t>(n) * c * out_h * out_w;
-  const int64_t index = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (index >= total) return;
-  const int ow = static_cast<int>(index % out_w);
-  const int64_t rest = index / out_w;
-  const int oh = static_cast<int>(rest % out_h);
-  const int64_t plane = rest / out_h;  // image * C + channel
-  const float* src = x + plane * h * w;
-  float best = -__builtin_huge_valf();
-  for (int kh = 0; kh < kernel_h; ++kh) {
-    const int ih = oh * stride_h - pad_h + kh * dilation_h;
-    if (static_cast<unsigned>(ih) >= static_cast<unsigned>(h)) continue;
-    const float* line = src + static_cast<int64_t>(ih) * w;
-    for (int kw = 0; kw < kernel_w; ++kw) {
-      const int iw = ow * stride_w - pad_w + kw * dilation_w;
-      if (static_cast<unsigned>(iw) < static_cast<unsigned>(w)) best = fmaxf(best, line[iw]);
+  __shared__ __attribute__((aligned(16))) float tile[kPoolLds];
+  const int bands = (out_h + kBand - 1) / kBand;
+  const int plane = blockIdx.x / bands;
+  const int band = blockIdx.x - plane * bands;
+  if (plane >= n * c) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int oh0 = band * kBand;
+  const int rows_out = min(kBand, out_h - oh0);
+  const int ih0 = oh0 * stride_h - pad_h;
+  const int rows_in = (rows_out - 1) * stride_h + (kernel_h - 1) * dilation_h + 1;
+  const bool staged = rows_in * w <= kPoolLds;
+  const float* src = x + static_cast<int64_t>(plane) * h * w;
+  float* dst = output + static_cast<int64_t>(plane) * out_h * out_w;
+  const float neg_inf = -__builtin_huge_valf();
+  if (staged) {
+    // The band's rows inside the image are one contiguous span of the
+    // plane: copied flat, 16 bytes per lane when rows are whole float4s.
+    const int first = max(ih0, 0);
+    const int last = min(ih0 + rows_in, h);  // exclusive
+    const int span = max(last - first, 0) * w;
+    float* to = tile + (first - ih0) * w;
+    const float* from = src + static_cast<int64_t>(first) * w;
+    if ((w & 3) == 0) {
+      const int span4 = span >> 2;
+      for (int i = threadIdx.x; i < span4; i += kThreads) {
+        reinterpret_cast<ct::f32x4*>(to)[i] = reinterpret_cast<const ct::f32x4*>(from)[i];
+      }
+    } else {
+      for (int i = threadIdx.x; i < span; i += kThreads) to[i] = from[i];
+    }
+    // Rows above or below the image read as -inf.
+    for (int r = wave; r < rows_in; r += kThreads / 64) {
+      const int ih = ih0 + r;
+      if (static_cast<unsigned>(ih) < static_cast<unsigned>(h)) continue;
+      for (int col = lane; col < w; col += 64) tile[r * w + col] = neg_inf;
+    }
+    __syncthreads();
+  }
+  for (int r = wave; r < rows_out; r += kThreads / 64) {
+    const int oh = oh0 + r;
+    for (int ow = lane; ow < out_w; ow += 64) {
+      float best = neg_inf;
+      for (int kh = 0; kh < kernel_h; ++kh) {
+        const int ih = oh * stride_h - pad_h + kh * dilation_h;
+        if (static_cast<unsigned>(ih) >= static_cast<unsigned>(h)) continue;
+        const float* line = staged ? tile + (ih - ih0) * w : src + static_cast<int64_t>(ih) * w;
+        for (int kw = 0; kw < kernel_w; ++kw) {
+          const int iw = ow * stride_w - pad_w + kw * dilation_w;
+          if (static_cast<unsigned>(iw) < static_cast<unsigned>(w)) best = fmaxf(best, line[iw]);
+        }
+      }
+      dst[static_cast<int64_t>(oh) * out_w + ow] = best;
     }
   }
-  output[index] = best;
 }
 
 // One wavefront reduces 64 consecutive (image, channel) planes. When a plane

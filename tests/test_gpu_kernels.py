@@ -245,6 +245,8 @@ def test_gemm_fp32(tmp_path, family, variant, m, k, n, bias):
     ((2, 64, 112, 112), 3, 2, 1),   # ResNet stem pool
     ((1, 5, 17, 14), 3, 2, 1),      # ragged
     ((2, 3, 9, 9), 2, 2, 0),        # no padding, even window
+    ((1, 2, 8, 3000), 3, 1, 1),     # band too wide for LDS: global reads
+    ((3, 4, 30, 7), 3, 1, 0),       # stride 1, bands with a ragged last one
 ])
 def test_max_pool_bit_exact(shape, kernel, stride, pad):
     rng = np.random.default_rng(5)
