@@ -77,14 +77,18 @@ CONV_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("family_variant", CONV_VARIANTS)
-@pytest.mark.parametrize("tail,kernel_base", [
-    ("relu", "conv_bn_relu.fp32.nchw"),
-    ("bn", "conv_bn.fp32.nchw"),
-    ("add_relu", "conv_bn_add_relu.fp32.nchw"),
-    ("conv", "conv.fp32.nchw"),
-])
-def test_conv_family_variants(tmp_path, family_variant, tail, kernel_base):
+CONV_TAILS = {"relu": "conv_bn_relu.fp32.nchw", "bn": "conv_bn.fp32.nchw",
+              "add_relu": "conv_bn_add_relu.fp32.nchw", "conv": "conv.fp32.nchw"}
+# Every tile variant runs the residual-join epilogue (BN + residual + ReLU,
+# the one that reads the most); every epilogue runs on one variant of each
+# family. The epilogue code is shared by all tiles of a family.
+CONV_CASES = [(fv, "add_relu") for fv in CONV_VARIANTS] + [
+    (fv, tail) for fv in ("mfma:m64n64", "splitk:m64n64s4", "direct:d64n64") for tail in ("relu", "bn", "conv")]
+
+
+@pytest.mark.parametrize("family_variant,tail", CONV_CASES)
+def test_conv_family_variants(tmp_path, family_variant, tail):
+    kernel_base = CONV_TAILS[tail]
     rng = np.random.default_rng(7)
     family, variant = family_variant.split(":")
     kernel_id = f"{kernel_base}.{family}"
@@ -287,8 +291,14 @@ def gemm16_graph(rng, m, k, n, gelu, bias):
     return g, {"a": rng.standard_normal((m, k)).astype(np.float16)}
 
 
-@pytest.mark.parametrize("family,variant", GEMM16_VARIANTS)
-@pytest.mark.parametrize("gelu,bias", [(False, False), (True, False), (False, True), (True, True)])
+# Every tile variant runs the bias + GELU epilogue; every epilogue runs on
+# one variant of each family.
+GEMM16_CASES = [(f, v, True, True) for f, v in GEMM16_VARIANTS] + [
+    (f, v, gelu, bias) for f, v in (("", "m128n128w4"), ("_kn", "m128n128k64"))
+    for gelu, bias in ((False, False), (True, False), (False, True))]
+
+
+@pytest.mark.parametrize("family,variant,gelu,bias", GEMM16_CASES)
 def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
     rng = np.random.default_rng(13)
     base = {(False, False): "gemm.fp16.mfma", (True, False): "gemm_gelu.fp16.mfma",
