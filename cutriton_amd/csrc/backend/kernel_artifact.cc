@@ -201,6 +201,9 @@ Status ArtifactRepository::Load(const std::vector<std::string>& paths) {
   repository_hash_.clear();
   if (paths.empty()) return Status::InvalidArgument("kernel artifact paths are empty");
   std::string digest_material;
+  // Variants of one kernel family share a code object: read and hash each
+  // file once per load.
+  std::unordered_map<std::string, std::string> file_digests;
   try {
     for (const auto& item : paths) {
       const std::filesystem::path given(item);
@@ -277,10 +280,14 @@ Status ArtifactRepository::Load(const std::vector<std::string>& paths) {
           throw std::runtime_error("unsafe Kernel Pack binary path");
         }
         a.binary_path = root / relative;
-        bool found = false;
-        const std::string image = ReadFile(a.binary_path, &found);
-        if (!found) return Status::NotFound("kernel binary not found: " + a.binary_path.string());
-        if (Sha256Hex(image) != a.sha256) {
+        auto digest = file_digests.find(a.binary_path.string());
+        if (digest == file_digests.end()) {
+          bool found = false;
+          const std::string image = ReadFile(a.binary_path, &found);
+          if (!found) return Status::NotFound("kernel binary not found: " + a.binary_path.string());
+          digest = file_digests.emplace(a.binary_path.string(), Sha256Hex(image)).first;
+        }
+        if (digest->second != a.sha256) {
           return Status::InvalidArgument("kernel binary SHA-256 mismatch: " +
                                          a.binary_path.string());
         }

@@ -441,6 +441,22 @@ void KernelPackAbi() {
       ++g_failures;
     }
   }
+  // Two variants share one code object: the file is hashed once per load,
+  // and each entry's sha256 is still checked against that digest.
+  {
+    const std::string text = PackText(2, v2_grid);
+    const size_t begin = text.find("{\n  \"kernel_id\"");
+    const size_t end = text.rfind("\n }") + 3;
+    std::string second = text.substr(begin, end - begin);
+    second.replace(second.find("\"only\""), 6, "\"second\"");
+    second.replace(second.find("\"default\": true"), 15, "\"default\": false");
+    write(text.substr(0, end) + ", " + second + text.substr(end));
+    EXPECT_OK(repo.Load({root.string()}));
+    EXPECT(repo.artifacts().size() == 2);
+    second.replace(second.find(kDummySha), 64, std::string(64, '0'));
+    write(text.substr(0, end) + ", " + second + text.substr(end));
+    EXPECT(repo.Load({root.string()}).code() == ErrorCode::kInvalidArgument);
+  }
   // Input layouts: OHWI on an input is accepted; any other layout, or a
   // layout on an output, is rejected.
   auto with_source = [&](const std::string& from, const std::string& to) {
