@@ -21,6 +21,7 @@
 #include "cutriton/runtime/engine.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -39,6 +40,7 @@
 #include "cutriton/core/buffer.h"
 #include "cutriton/ir/pass.h"
 #include "cutriton_hip_runtime.h"
+#include "runtime/relayout.h"
 
 namespace cutriton {
 namespace {
@@ -276,6 +278,24 @@ std::optional<std::size_t> FindCandidate(const PlanOp& op, const std::string& id
 
 }  // namespace
 
+// CUTRITON_INIT_LOG=1 prints the wall time of each one-time stage of a
+// context's first run: constant upload and re-layout, tuning, kernel
+// loading, graph capture.
+class StageTimer {
+ public:
+  explicit StageTimer(const char* stage) : stage_(stage), start_(std::chrono::steady_clock::now()) {}
+  ~StageTimer() {
+    static const bool enabled = std::getenv("CUTRITON_INIT_LOG") != nullptr;
+    if (!enabled) return;
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start_).count();
+    if (ms >= 0.05) std::fprintf(stderr, "[cutriton init] %s: %.2f ms\n", stage_, ms);
+  }
+
+ private:
+  const char* stage_;
+  std::chrono::steady_clock::time_point start_;
+};
+
 class EngineState {
  public:
   explicit EngineState(ExecutablePlan p) : plan(std::move(p)) {}
@@ -300,31 +320,37 @@ class EngineState {
  private:
   Status UploadConstants() {
     const Device& device = plan.backend_options().device;
-    for (const auto& entry : plan.constants()) {
-      const ValueDesc* value = plan.graph().FindValue(entry.first);
-      if (value == nullptr || !value->is_constant) {
-        return Status::Internal("plan constant is missing from the graph: " + entry.first);
+    {
+      StageTimer timer("constant upload");
+      for (const auto& entry : plan.constants()) {
+        const ValueDesc* value = plan.graph().FindValue(entry.first);
+        if (value == nullptr || !value->is_constant) {
+          return Status::Internal("plan constant is missing from the graph: " + entry.first);
+        }
+        if (device.type == DeviceType::kCPU) {
+          device_constants.emplace(entry.first, entry.second);
+          continue;
+        }
+        std::shared_ptr<Buffer> buffer;
+        CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(value->tensor.ByteSize(), device.id, &buffer));
+        const Tensor& host = entry.second;
+        const auto* bytes = static_cast<const std::uint8_t*>(host.buffer()->data()) + host.byte_offset();
+        CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(bytes, value->tensor.ByteSize()));
+        device_constants.emplace(entry.first, Tensor(value->tensor, std::move(buffer)));
       }
-      if (device.type == DeviceType::kCPU) {
-        device_constants.emplace(entry.first, entry.second);
-        continue;
-      }
-      std::shared_ptr<Buffer> buffer;
-      CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(value->tensor.ByteSize(), device.id, &buffer));
-      const Tensor& host = entry.second;
-      const auto* bytes = static_cast<const std::uint8_t*>(host.buffer()->data()) + host.byte_offset();
-      CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(bytes, value->tensor.ByteSize()));
-      device_constants.emplace(entry.first, Tensor(value->tensor, std::move(buffer)));
     }
     return UploadLaidOutConstants();
   }
 
   // Copies of constants in the layout a selected kernel reads them in (the
-  // KernelInvocation input "<constant>#<layout>"), made once per engine.
-  // The copy keeps the logical shape; only the element order changes.
+  // KernelInvocation input "<constant>#<layout>"), made once per engine on
+  // the device from the uploaded original. The copy keeps the logical
+  // shape; only the element order changes.
   Status UploadLaidOutConstants() {
     const Device& device = plan.backend_options().device;
     if (device.type != DeviceType::kHIP) return Status::OK();
+    StageTimer timer("constant re-layout");
+    bool launched = false;
     for (const PlanOp& op : plan.ops()) {
       for (const ExecutionCandidate& candidate : op.candidates) {
         for (const PlanStep& step : candidate.steps) {
@@ -338,51 +364,35 @@ class EngineState {
             const std::string& name = inv->inputs[static_cast<std::size_t>(src.index)];
             if (device_constants.count(name) != 0) continue;
             const std::string base = name.substr(0, name.rfind('#'));
-            const auto host = plan.constants().find(base);
-            if (host == plan.constants().end() || !IsInputLayout(src.layout)) {
+            const auto original = device_constants.find(base);
+            if (original == device_constants.end() || !IsInputLayout(src.layout)) {
               return Status::Internal("no constant to lay out as " + name);
             }
-            const TensorDesc& desc = host->second.desc();
+            const TensorDesc& desc = original->second.desc();
             TensorDesc laid_out = desc;
             laid_out.layout = src.layout;
-            const auto* in_bytes =
-                static_cast<const std::uint8_t*>(host->second.buffer()->data()) + host->second.byte_offset();
-            std::vector<std::uint8_t> out(desc.ByteSize());
             if (src.layout == "OHWI") {
               if (desc.shape.size() != 4 || desc.dtype != DataType::kFloat32) {
                 return Status::InvalidArgument("OHWI needs a rank-4 float32 constant: " + base);
               }
-              const int64_t k = desc.shape[0], c = desc.shape[1], r = desc.shape[2], w = desc.shape[3];
-              if (r * w == 1) {  // [K][C][1][1]: both orders are the same bytes
-                device_constants.emplace(name, Tensor(laid_out, device_constants.at(base).buffer(),
-                                                      device_constants.at(base).byte_offset()));
+              if (desc.shape[2] * desc.shape[3] == 1) {  // [K][C][1][1]: both orders are the same bytes
+                device_constants.emplace(name, Tensor(laid_out, original->second.buffer(),
+                                                      original->second.byte_offset()));
                 continue;
               }
-              const auto* in = reinterpret_cast<const float*>(in_bytes);
-              auto* o = reinterpret_cast<float*>(out.data());
-              for (int64_t oc = 0; oc < k; ++oc)
-                for (int64_t i = 0; i < c; ++i)
-                  for (int64_t y = 0; y < r; ++y)
-                    for (int64_t x = 0; x < w; ++x)
-                      o[static_cast<std::size_t>(((oc * r + y) * w + x) * c + i)] =
-                          in[static_cast<std::size_t>(((oc * c + i) * r + y) * w + x)];
-            } else {  // NK: [K][N] -> [N][K], any element size
-              if (desc.shape.size() != 2) return Status::InvalidArgument("NK needs a rank-2 constant: " + base);
-              const int64_t kd = desc.shape[0], nd = desc.shape[1];
-              const std::size_t es = ElementSize(desc.dtype);
-              for (int64_t row = 0; row < kd; ++row)
-                for (int64_t col = 0; col < nd; ++col)
-                  std::memcpy(out.data() + static_cast<std::size_t>(col * kd + row) * es,
-                              in_bytes + static_cast<std::size_t>(row * nd + col) * es, es);
             }
             std::shared_ptr<Buffer> buffer;
             CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(desc.ByteSize(), device.id, &buffer));
-            CUTRITON_RETURN_IF_ERROR(buffer->CopyFromHost(out.data(), desc.ByteSize()));
+            const auto* in = static_cast<const std::uint8_t*>(original->second.buffer()->data()) +
+                             original->second.byte_offset();
+            CUTRITON_RETURN_IF_ERROR(RelayoutOnDevice(src.layout, desc, in, buffer->data(), device.id));
+            launched = true;
             device_constants.emplace(name, Tensor(laid_out, std::move(buffer)));
           }
         }
       }
     }
+    if (launched) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_device_synchronize(device.id), "hipDeviceSynchronize"));
     return Status::OK();
   }
 
@@ -930,10 +940,19 @@ Status ExecutionContext::CaptureGraph(void* stream, void** exec) {
 
 Status ExecutionContext::RunAsync(void* stream) {
   if (run_pending_) return Status::RuntimeError("a run is already pending");
-  CUTRITON_RETURN_IF_ERROR(PrepareTensors());
+  {
+    StageTimer timer("tensors");
+    CUTRITON_RETURN_IF_ERROR(PrepareTensors());
+  }
   CUTRITON_RETURN_IF_ERROR(ValidateBindings());
-  CUTRITON_RETURN_IF_ERROR(PrepareTuning());
-  CUTRITON_RETURN_IF_ERROR(PrepareKernels());
+  {
+    StageTimer timer("tuning");
+    CUTRITON_RETURN_IF_ERROR(PrepareTuning());
+  }
+  {
+    StageTimer timer("kernel loading");
+    CUTRITON_RETURN_IF_ERROR(PrepareKernels());
+  }
 
   const Device& device = state_->plan.backend_options().device;
   if (device.type != DeviceType::kHIP) {
@@ -984,6 +1003,7 @@ Status ExecutionContext::RunAsync(void* stream) {
   if (entry == hip->graphs.end()) {
     GraphEntry created;
     created.key = graph_key;
+    StageTimer timer("graph capture");
     CUTRITON_RETURN_IF_ERROR(CaptureGraph(hip->active_stream, &created.exec));
     const std::size_t capacity = std::max<std::size_t>(1, state_->plan.hip_graph_cache_capacity());
     if (hip->graphs.size() >= capacity) {

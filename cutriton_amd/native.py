@@ -1,9 +1,10 @@
 """Build and load the native pieces: the C++ engine library and the Kernel Pack.
 
 ``build_all()`` compiles ``csrc/**/*.cc`` (host C++17 against the HIP runtime)
-into ``libcutriton_gfx950.so`` beside this file and runs the pack producer
-into ``pack/``. ``library()`` loads the engine library and raises when it is
-missing: there is no fallback path.
+into ``libcutriton_gfx950.so`` beside this file, with the engine's own
+re-layout kernels (``csrc/runtime/relayout.hip``, gfx950) embedded as a code
+object, and runs the pack producer into ``pack/``. ``library()`` loads the
+engine library and raises when it is missing: there is no fallback path.
 """
 
 from __future__ import annotations
@@ -39,11 +40,37 @@ def _compile(source: Path) -> Path:
     return obj
 
 
+def _embedded_relayout_code() -> Path:
+    """Compiles ``relayout.hip`` to a gfx950 code object and compiles that
+    object into the library as ``cutriton::kRelayoutCodeObject``."""
+    from .kernel_sdk.builder import compile_code_object
+
+    hsaco = BUILD_DIR / "relayout.hsaco"
+    compile_code_object(CSRC_DIR / "runtime" / "relayout.hip", hsaco)
+    data = hsaco.read_bytes()
+    rows = [", ".join(str(b) for b in data[i:i + 32]) for i in range(0, len(data), 32)]
+    source = BUILD_DIR / "relayout_code.cc"
+    source.write_text(
+        "// Generated from csrc/runtime/relayout.hip by cutriton_amd/native.py.\n"
+        "#include <cstddef>\n\nnamespace cutriton {\n"
+        "extern const unsigned char kRelayoutCodeObject[];\n"
+        "extern const std::size_t kRelayoutCodeObjectBytes;\n"
+        "alignas(64) const unsigned char kRelayoutCodeObject[] = {\n" + ",\n".join(rows) + "};\n"
+        "const std::size_t kRelayoutCodeObjectBytes = sizeof(kRelayoutCodeObject);\n"
+        "}  // namespace cutriton\n")
+    obj = BUILD_DIR / "relayout_code.o"
+    result = subprocess.run(["g++", *CXXFLAGS, "-c", str(source), "-o", str(obj)], capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"g++ failed for {source}:\n{result.stderr}")
+    return obj
+
+
 def build_engine_library(jobs: int = 8) -> Path:
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC_DIR.rglob("*.cc"))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(_compile, sources))
+        embedded = pool.submit(_embedded_relayout_code)
+        objects = list(pool.map(_compile, sources)) + [embedded.result()]
     staging = LIBRARY_PATH.with_suffix(".so.tmp")
     cmd = ["g++", "-shared", "-o", str(staging), *map(str, objects),
            f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"]
