@@ -6,6 +6,9 @@ Workloads (synthetic seeded inputs, random-init weights of the named shapes):
     GAP, Flatten view, Gemm), replayed as one hipGraph. `value` is img/s.
   * FP16 FFN block M=4096, H=1024, I=4096 (GemmGelu -> Gemm -> SkipLayerNorm):
     reported as TFLOP/s of its two GEMMs beside the main line.
+  * FP16 Softmax over attention scores [16*16*1024, 1024] and a standalone
+    FP16 LayerNorm of the same shape: reported as GB/s (HBM-bound) beside the
+    main line.
 
 Timing: the first run tunes every op (TuneOnMiss, cache in a temporary
 directory). Then W untimed warm-up steps and K timed steps bracketed by
@@ -221,6 +224,41 @@ def bench_ffn(args, cache_dir: str) -> dict:
     return out
 
 
+def bench_norms(args, cache_dir: str) -> dict:
+    """Softmax over attention scores (16 sequences x 16 heads x 1024 queries,
+    1024 keys) and a standalone LayerNorm of the same [262144, 1024] shape,
+    FP16: each reads and writes 512 MiB once (the LayerNorm's scale and bias
+    add 4 KiB). 512 MiB exceeds the 256 MB Infinity Cache, so back-to-back
+    launches stream from HBM."""
+    import numpy as np
+
+    from cutriton_amd import workloads
+
+    rows, columns = 16 * 16 * 1024, 1024
+    rng = np.random.default_rng(workloads.SEED)
+    x = (rng.standard_normal((rows, columns), dtype=np.float32) * 4).astype(np.float16)
+    out: dict = {"softmax_shape": [rows, columns], "layer_norm_shape": [rows, columns]}
+    moved = 2 * rows * columns * 2
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((rows, columns), "float16", "")
+    g.add("softmax", "Softmax", ["x"], ["y"], axis=-1)
+    g.outputs.append("y")
+    _, kernel_ms, _, _, selected = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    out.update(softmax_us=kernel_ms[0] * 1e3, softmax_gbps=moved / (kernel_ms[0] * 1e-3) / 1e9,
+               softmax_variant=selected[0].rsplit(":", 1)[1])
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((rows, columns), "float16", "")
+    gamma = g.constant("gamma", rng.uniform(0.5, 1.5, columns).astype(np.float16))
+    beta = g.constant("beta", rng.normal(0.0, 0.1, columns).astype(np.float16))
+    g.add("ln", "LayerNormalization", ["x", gamma, beta], ["y"], axis=-1, epsilon=1e-5)
+    g.outputs.append("y")
+    _, kernel_ms, _, _, _ = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    out.update(layer_norm_us=kernel_ms[0] * 1e3, layer_norm_gbps=(moved + 4 * columns) / (kernel_ms[0] * 1e-3) / 1e9)
+    log(f"  softmax: {out['softmax_us']:.1f} us ({out['softmax_gbps']:.0f} GB/s, {out['softmax_variant']}); "
+        f"layer norm: {out['layer_norm_us']:.1f} us ({out['layer_norm_gbps']:.0f} GB/s)")
+    return out
+
+
 def bench_copy(args, cache_dir: str) -> dict:
     """One Relu over 64 Mi non-negative floats: the relu_fp32 kernel reads and
     writes exactly 256 MiB each. Its GB/s is the streaming reference for the
@@ -290,7 +328,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "copy"), default="all")
+    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "norms", "copy"), default="all")
     parser.add_argument("--tuning-cache", default="",
                         help="tuning cache folder to reuse (default: a fresh temporary folder, so every op is tuned)")
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
@@ -327,6 +365,13 @@ def main() -> int:
         if args.workload == "ffn":
             result.update(value=round(f["tflops_block"], 3), unit="TFLOP/s", ms_per_step=round(f["ms_per_step"], 4),
                           dtype="fp16", config={"workload": f["workload"], "parallelism": "single-gpu"})
+    if args.workload in ("all", "norms"):
+        n = bench_norms(args, cache_dir)
+        result["norms"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in n.items()}
+        if args.workload == "norms":
+            result.update(value=round(n["softmax_gbps"], 1), unit="GB/s", dtype="fp16",
+                          ms_per_step=round(n["softmax_us"] * 1e-3, 4),
+                          config={"workload": "softmax_fp16_262144x1024", "parallelism": "single-gpu"})
     if args.workload == "copy":
         c = bench_copy(args, cache_dir)
         result.update(value=round(c["gbps"], 1), unit="GB/s", ms_per_step=round(c["ms_per_step"], 4),

@@ -185,6 +185,21 @@ Status InferLayerNormalization(Graph* graph, const Node& node) {
   return graph->SetValueDesc(node.outputs()[0], x->tensor);
 }
 
+// Softmax over the last axis only: the reference's kernel ignores `axis`
+// (python/cutriton/triton_kernels/transformer.py:180-190) and would give a
+// last-axis result for any other axis; here another axis is refused.
+Status InferSoftmax(Graph* graph, const Node& node) {
+  const ValueDesc* x = node.inputs().size() == 1 ? graph->FindValue(node.inputs()[0]) : nullptr;
+  if (x == nullptr || x->tensor.shape.empty() || node.outputs().size() != 1) {
+    return Status::ShapeError("Softmax expects one input of rank >= 1 and one output");
+  }
+  const int64_t axis = GetIntAttribute(node, "axis", -1);
+  if (axis != -1 && axis != static_cast<int64_t>(x->tensor.shape.size()) - 1) {
+    return Status::Unsupported("only last-axis Softmax is supported");
+  }
+  return graph->SetValueDesc(node.outputs()[0], x->tensor);
+}
+
 Status InferSkipLayerNormalization(Graph* graph, const Node& node) {
   if (node.inputs().size() != 4) {
     return Status::ShapeError("SkipLayerNormalization expects input, residual, scale and bias");
@@ -501,9 +516,10 @@ Status RegisterBuiltinOpSchemas() {
   CUTRITON_RETURN_IF_ERROR(add("FusedConvBatchNormRelu", 6, 6, InferConvLike));
   CUTRITON_RETURN_IF_ERROR(add("FusedConvBatchNormAddRelu", 7, 7, InferConvResidual));
   CUTRITON_RETURN_IF_ERROR(add("BatchNormalization", 5, 5, InferSameAsFirstInput));
-  for (const char* op : {"Relu", "Gelu", "Softmax"}) {
+  for (const char* op : {"Relu", "Gelu"}) {
     CUTRITON_RETURN_IF_ERROR(add(op, 1, 1, InferSameAsFirstInput));
   }
+  CUTRITON_RETURN_IF_ERROR(add("Softmax", 1, 1, InferSoftmax));
   CUTRITON_RETURN_IF_ERROR(add("LayerNormalization", 2, 3, InferLayerNormalization));
   CUTRITON_RETURN_IF_ERROR(add("Add", 2, 2, InferElementwiseBinary));
   CUTRITON_RETURN_IF_ERROR(add("AddRelu", 2, 2, InferElementwiseBinary));

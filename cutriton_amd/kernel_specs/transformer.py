@@ -15,7 +15,6 @@ from cutriton_amd.kernel_sdk.spec import (
     KernelVariant,
     arg,
     ceil_div,
-    literal,
     meta,
     mul,
     numel_grid,
@@ -138,6 +137,17 @@ def register_elementwise() -> None:
         ))
 
 
+# Row-kernel variants of LayerNorm, SkipLayerNorm and Softmax: (name, rows
+# per 256-thread workgroup). gNcM: N lanes per row, M 16-byte chunks per lane;
+# rows of up to N * 8 * M columns stay in registers, longer rows re-read.
+ROW_VARIANTS = (
+    ("g16c1", 16), ("g32c1", 8), ("g64c1", 4), ("g64c2", 4), ("g64c4", 4), ("g64c8", 4),
+)
+ROW_DEFAULT = "g64c8"
+SOFTMAX_VARIANTS = ROW_VARIANTS
+SOFTMAX_DEFAULT = ROW_DEFAULT
+
+
 def register_norms() -> None:
     for kernel_id, op_type, symbol, inputs in (
         ("layer_norm.fp16.last_axis", "LayerNormalization", "layer_norm_fp16", ("x", "scale", "bias")),
@@ -150,11 +160,11 @@ def register_norms() -> None:
             arg("columns", "i32", "input_dim", index=0, axis=1),
             arg("epsilon", "fp32", "attribute_f64", name="epsilon", default=1e-5),
         ) + reserved()
-        # One wavefront per row, four rows per workgroup.
         register(KernelSpec(
             kernel_id, op_type, 1, "layer_norm_fp16.hip", arguments,
-            (ceil_div(output_dim(0), literal(4)),),
-            (KernelVariant("wave_per_row", symbol, num_warps=4, default=True),),
+            (ceil_div(output_dim(0), meta("ROWS")),),
+            tuple(KernelVariant(name, f"{symbol}_{name}", num_warps=4, meta={"ROWS": rows},
+                                default=name == ROW_DEFAULT) for name, rows in ROW_VARIANTS),
             dtype="float16",
             constraints=(
                 {"kind": "input_count_eq", "value": len(inputs)},
@@ -163,6 +173,29 @@ def register_norms() -> None:
         ))
 
 
+
+
+def register_softmax() -> None:
+    arguments = (
+        arg("x", "*fp16", "input", index=0),
+        arg("output", "*fp16", "output", index=0),
+        arg("rows", "i32", "input_dim", index=0, axis=0),
+        arg("columns", "i32", "input_dim", index=0, axis=1),
+    ) + reserved()
+    register(KernelSpec(
+        "softmax.fp16.last_axis", "Softmax", 1, "softmax_fp16.hip", arguments,
+        (ceil_div(output_dim(0), meta("ROWS")),),
+        tuple(KernelVariant(name, f"softmax_fp16_{name}", num_warps=4, meta={"ROWS": rows},
+                            default=name == SOFTMAX_DEFAULT) for name, rows in SOFTMAX_VARIANTS),
+        dtype="float16",
+        constraints=(
+            {"kind": "input_count_eq", "value": 1},
+            {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+        ),
+    ))
+
+
 register_gemms()
 register_elementwise()
 register_norms()
+register_softmax()

@@ -38,6 +38,12 @@ __device__ __forceinline__ float WaveSum(float v) {
   return v;
 }
 
+__device__ __forceinline__ float WaveMax(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+  return v;
+}
+
 // erf-GELU in FP32: 0.5 * a * (1 + erf(a / sqrt(2))), with ROCm's erff.
 __device__ __forceinline__ float GeluErf(float a) {
   return 0.5f * a * (1.0f + erff(a * 0.7071067811865476f));

@@ -1,30 +1,45 @@
 // LayerNormalization and SkipLayerNormalization over the last axis, FP16 in
-// and out, FP32 statistics; one wavefront per row.
+// and out, FP32 statistics.
 //
 // Semantics follow python/cutriton/triton_kernels/transformer.py:
 //   layer_norm_fp16 (128-149) and skip_layer_norm_fp16 (152-177):
 //   v = x (+ residual), widened to FP32; mean = sum(v) / cols;
 //   var = sum((v - mean)^2) / cols (two passes over the row);
 //   y = fp16((v - mean) * rsqrt(var + eps) * gamma + beta).
-// Unlike the reference (one 1024-wide block per row) any column count works:
-// rows of up to kCachedColumns stay in registers between the passes, longer
-// rows are re-read. Argument order is the pack ABI of transformer.py:323-371.
+// Unlike the reference (one 1024-wide block per row) any column count works.
+// A group of GROUP lanes owns one row (64 / GROUP rows per wavefront); each
+// lane keeps CHUNKS 16-byte chunks of the row in registers between the two
+// passes, so x (and the residual) are read once. Rows longer than
+// GROUP * 8 * CHUNKS columns, or not 16-byte aligned, are re-read from
+// global memory. Variants differ only in GROUP and CHUNKS: fewer chunks use
+// fewer registers and keep more rows in flight. Argument order is the pack
+// ABI of transformer.py:323-371.
 #include "common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerBlock = kThreads / 64;
-constexpr int kChunk = 8;                                   // halves per lane per 16-byte access
-constexpr int kCachedChunks = 8;                            // 16-byte chunks per lane kept in registers
-constexpr int kCachedColumns = 64 * kChunk * kCachedChunks;  // 4096
+constexpr int kChunk = 8;  // halves per 16-byte access
 
-template <bool SKIP>
+template <int GROUP>
+__device__ __forceinline__ float GroupSum(float v) {
+#pragma unroll
+  for (int offset = GROUP / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+template <int GROUP, int CHUNKS, bool SKIP>
 __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, const _Float16* __restrict__ residual,
                                              const _Float16* __restrict__ gamma, const _Float16* __restrict__ beta,
                                              _Float16* __restrict__ output, int rows, int columns, float epsilon) {
+  static_assert(GROUP == 16 || GROUP == 32 || GROUP == 64, "a row group is 16, 32 or 64 lanes");
+  constexpr int kRowsPerWave = 64 / GROUP;
+  constexpr int kRowsPerBlock = (kThreads / 64) * kRowsPerWave;
+  constexpr int kCachedColumns = GROUP * kChunk * CHUNKS;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int sub = lane % GROUP;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6) * kRowsPerWave + lane / GROUP;
+  // Whole groups leave together; the shuffles below stay inside a group.
   if (row >= rows) return;
   const size_t offset = static_cast<size_t>(row) * columns;
   const _Float16* xr = x + offset;
@@ -37,11 +52,11 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
                      (SKIP ? reinterpret_cast<uintptr_t>(residual) : 0)) & 15) == 0;
 
   if (vec) {
-    float v[kCachedChunks][kChunk];
+    float v[CHUNKS][kChunk];
     float sum = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kCachedChunks; ++c) {
-      const int col = (c * 64 + lane) * kChunk;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int col = (c * GROUP + sub) * kChunk;
       if (col < columns) {
         const ct::f16x8 a = *reinterpret_cast<const ct::f16x8*>(xr + col);
         ct::f16x8 b;
@@ -53,11 +68,11 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
         }
       }
     }
-    const float mean = ct::WaveSum(sum) * inv_columns;
+    const float mean = GroupSum<GROUP>(sum) * inv_columns;
     float sq = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kCachedChunks; ++c) {
-      const int col = (c * 64 + lane) * kChunk;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int col = (c * GROUP + sub) * kChunk;
       if (col < columns) {
 #pragma unroll
         for (int e = 0; e < kChunk; ++e) {
@@ -66,10 +81,10 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
         }
       }
     }
-    const float rstd = rsqrtf(ct::WaveSum(sq) * inv_columns + epsilon);
+    const float rstd = rsqrtf(GroupSum<GROUP>(sq) * inv_columns + epsilon);
 #pragma unroll
-    for (int c = 0; c < kCachedChunks; ++c) {
-      const int col = (c * 64 + lane) * kChunk;
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int col = (c * GROUP + sub) * kChunk;
       if (col < columns) {
         const ct::f16x8 g = *reinterpret_cast<const ct::f16x8*>(gamma + col);
         const ct::f16x8 bt = *reinterpret_cast<const ct::f16x8*>(beta + col);
@@ -89,15 +104,15 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
     return static_cast<float>(xr[col]) + (SKIP ? static_cast<float>(rr[col]) : 0.0f);
   };
   float sum = 0.0f;
-  for (int col = lane; col < columns; col += 64) sum += value(col);
-  const float mean = ct::WaveSum(sum) * inv_columns;
+  for (int col = sub; col < columns; col += GROUP) sum += value(col);
+  const float mean = GroupSum<GROUP>(sum) * inv_columns;
   float sq = 0.0f;
-  for (int col = lane; col < columns; col += 64) {
+  for (int col = sub; col < columns; col += GROUP) {
     const float d = value(col) - mean;
     sq += d * d;
   }
-  const float rstd = rsqrtf(ct::WaveSum(sq) * inv_columns + epsilon);
-  for (int col = lane; col < columns; col += 64) {
+  const float rstd = rsqrtf(GroupSum<GROUP>(sq) * inv_columns + epsilon);
+  for (int col = sub; col < columns; col += GROUP) {
     yr[col] = static_cast<_Float16>((value(col) - mean) * rstd * static_cast<float>(gamma[col]) +
                                     static_cast<float>(beta[col]));
   }
@@ -105,14 +120,24 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
 
 }  // namespace
 
-CT_KERNEL void __launch_bounds__(kThreads)
-    layer_norm_fp16(const _Float16* x, const _Float16* scale, const _Float16* bias, _Float16* output, int rows,
-                    int columns, float epsilon, void*, void*) {
-  LayerNormRow<false>(x, nullptr, scale, bias, output, rows, columns, epsilon);
-}
+#define CT_DEFINE_LAYER_NORM(NAME, GROUP, CHUNKS)                                                                   \
+  CT_KERNEL void __launch_bounds__(kThreads)                                                                       \
+      layer_norm_fp16_##NAME(const _Float16* x, const _Float16* scale, const _Float16* bias, _Float16* output,      \
+                             int rows, int columns, float epsilon, void*, void*) {                                 \
+    LayerNormRow<GROUP, CHUNKS, false>(x, nullptr, scale, bias, output, rows, columns, epsilon);                    \
+  }                                                                                                                \
+  CT_KERNEL void __launch_bounds__(kThreads)                                                                       \
+      skip_layer_norm_fp16_##NAME(const _Float16* x, const _Float16* residual, const _Float16* scale,              \
+                                  const _Float16* bias, _Float16* output, int rows, int columns, float epsilon,    \
+                                  void*, void*) {                                                                  \
+    LayerNormRow<GROUP, CHUNKS, true>(x, residual, scale, bias, output, rows, columns, epsilon);                   \
+  }
 
-CT_KERNEL void __launch_bounds__(kThreads)
-    skip_layer_norm_fp16(const _Float16* x, const _Float16* residual, const _Float16* scale, const _Float16* bias,
-                         _Float16* output, int rows, int columns, float epsilon, void*, void*) {
-  LayerNormRow<true>(x, residual, scale, bias, output, rows, columns, epsilon);
-}
+// NAME: lanes per row (g) and 16-byte chunks per lane (c); rows of up to
+// g * 8 * c columns stay in registers.
+CT_DEFINE_LAYER_NORM(g16c1, 16, 1)
+CT_DEFINE_LAYER_NORM(g32c1, 32, 1)
+CT_DEFINE_LAYER_NORM(g64c1, 64, 1)
+CT_DEFINE_LAYER_NORM(g64c2, 64, 2)
+CT_DEFINE_LAYER_NORM(g64c4, 64, 4)
+CT_DEFINE_LAYER_NORM(g64c8, 64, 8)

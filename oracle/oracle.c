@@ -15,6 +15,8 @@
  *   ct_oracle_gelu            transformer.py:110-116 (0.5 x (1 + erf(x/sqrt 2)))
  *   ct_oracle_layer_norm      transformer.py:128-177 (optional residual;
  *                             two-pass mean / centred variance; eps inside sqrt)
+ *   ct_oracle_softmax         transformer.py:180-190 (last axis; subtract the
+ *                             row max, exp, divide by the sum)
  * Parity pins (closed forms, invariants, brute force, torch float64) are in
  * tests/test_oracle.py.
  */
@@ -134,3 +136,21 @@ void ct_oracle_layer_norm(const double* x, const double* residual, long rows, lo
     for (long j = 0; j < cols; ++j) yr[j] = (xr[j] + (rr ? rr[j] : 0.0) - mean) * inv * gamma[j] + beta[j];
   }
 }
+
+/* Row softmax over the last axis: e_j = exp(x_j - max_i x_i), y_j = e_j / sum e.
+ * A row of -inf entries gives NaN (-inf - -inf), as the reference does. */
+void ct_oracle_softmax(const double* x, long rows, long cols, double* out) {
+  for (long r = 0; r < rows; ++r) {
+    const double* xr = x + (size_t)r * cols;
+    double* yr = out + (size_t)r * cols;
+    double max = -INFINITY;
+    for (long j = 0; j < cols; ++j) max = xr[j] > max ? xr[j] : max;
+    double sum = 0.0;
+    for (long j = 0; j < cols; ++j) {
+      yr[j] = exp(xr[j] - max);
+      sum += yr[j];
+    }
+    for (long j = 0; j < cols; ++j) yr[j] /= sum;
+  }
+}
+

@@ -55,8 +55,9 @@ def _lib() -> ctypes.CDLL:
         lib.ct_oracle_gemm.argtypes = [D, D, D, I, I, I, D]
         lib.ct_oracle_gelu.argtypes = [D, L, D]
         lib.ct_oracle_layer_norm.argtypes = [D, D, L, L, D, D, ctypes.c_double, D]
+        lib.ct_oracle_softmax.argtypes = [D, L, L, D]
         for fn in ("ct_oracle_conv2d", "ct_oracle_batch_norm", "ct_oracle_max_pool", "ct_oracle_global_avg_pool",
-                   "ct_oracle_gemm", "ct_oracle_gelu", "ct_oracle_layer_norm"):
+                   "ct_oracle_gemm", "ct_oracle_gelu", "ct_oracle_layer_norm", "ct_oracle_softmax"):
             getattr(lib, fn).restype = None
         _LIB = lib
     return _LIB
@@ -146,6 +147,15 @@ def layer_norm(x: np.ndarray, gamma, beta, eps: float, residual: np.ndarray | No
     return out
 
 
+def softmax(x: np.ndarray) -> np.ndarray:
+    """Softmax over the last axis."""
+    x = _d(x)
+    cols = x.shape[-1]
+    out = np.empty_like(x)
+    _lib().ct_oracle_softmax(_p(x), x.size // cols if cols else 0, cols, _p(out))
+    return out
+
+
 def _ints(attrs: Mapping[str, Any], key: str, default):
     value = attrs.get(key, default)
     return list(value) if isinstance(value, (list, tuple)) else value
@@ -197,6 +207,10 @@ def evaluate(graph: Any, feeds: Mapping[str, np.ndarray]) -> dict[str, np.ndarra
             y = layer_norm(ins[0], ins[1], ins[2], a.get("epsilon", 1e-5))
         elif op == "SkipLayerNormalization":
             y = layer_norm(ins[0], ins[2], ins[3], a.get("epsilon", 1e-5), residual=ins[1])
+        elif op == "Softmax":
+            if a.get("axis", -1) not in (-1, ins[0].ndim - 1):
+                raise NotImplementedError("the oracle's Softmax is over the last axis")
+            y = softmax(ins[0])
         else:
             raise NotImplementedError(f"oracle has no rule for {op}")
         env[node.outputs[0]] = y

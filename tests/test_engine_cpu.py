@@ -120,6 +120,31 @@ def test_ffn_pattern_plan(gfx950):
     assert [op.op_type for op in ops] == ["GemmGelu", "SkipLayerNormalization"]
 
 
+def softmax_model(axis: int):
+    g = workloads.GraphSpec()
+    g.inputs["x"] = ((2048, 512), "float16", "")
+    g.add("softmax", "Softmax", ["x"], ["y"], axis=axis)
+    g.outputs.append("y")
+    return workloads.to_model(g)
+
+
+def test_softmax_plan(gfx950):
+    from cutriton_amd.kernel_specs.transformer import SOFTMAX_DEFAULT, SOFTMAX_VARIANTS
+
+    ops = engine.build_engine(softmax_model(-1), engine.CompileOptions()).ops()
+    assert [op.op_type for op in ops] == ["Softmax"]
+    assert [c.rsplit(":", 1)[1] for c in ops[0].candidates] == [name for name, _ in SOFTMAX_VARIANTS]
+    assert ops[0].candidates[ops[0].selected_candidate].endswith("softmax.fp16.last_axis:" + SOFTMAX_DEFAULT)
+    assert len(engine.build_engine(softmax_model(1), engine.CompileOptions()).ops()) == 1
+
+
+def test_softmax_over_another_axis_is_refused(gfx950):
+    # The reference's kernel would compute the last-axis softmax here.
+    with pytest.raises(engine.CutritonError) as err:
+        engine.build_engine(softmax_model(0), engine.CompileOptions())
+    assert err.value.kind == "Unsupported"
+
+
 def test_shape_profiles_resolve_on_cpu(gfx950):
     graph = workloads.resnet50(1)
     opts = engine.CompileOptions(shape_profiles={"batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224),

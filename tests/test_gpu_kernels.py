@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from cutriton_amd import engine, workloads
+from cutriton_amd.kernel_specs.transformer import ROW_VARIANTS
 from oracle import oracle
 from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant, only_variant, run_graph,
                            without_kernels)
@@ -383,10 +384,7 @@ def test_gemm_fp16_activation_operand_uses_b_as_is():
     assert err.max() <= 1e-2, err.max()
 
 
-@pytest.mark.parametrize("rows,cols", [(512, 768), (17, 100), (4, 5000), (64, 1024)])
-@pytest.mark.parametrize("skip", [False, True])
-def test_layer_norm_fp16(rows, cols, skip):
-    rng = np.random.default_rng(17)
+def layer_norm_graph(rng, rows, cols, skip):
     g = workloads.GraphSpec()
     g.inputs["x"] = ((rows, cols), "float16", "")
     feeds = {"x": rng.standard_normal((rows, cols)).astype(np.float16)}
@@ -399,10 +397,26 @@ def test_layer_norm_fp16(rows, cols, skip):
         y = g.add("add", "Add", ["x", "r"], ["s"])
     g.add("ln", "LayerNormalization", [y, gamma, beta], ["y"], axis=-1, epsilon=1e-5)
     g.outputs.append("y")
-    out, eng, _ = run_graph(g, feeds)
-    assert [op.op_type for op in eng.ops()] == (["SkipLayerNormalization"] if skip else ["LayerNormalization"])
-    err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, feeds)["y"])
-    assert err.max() <= 1e-2, f"layer norm {rows}x{cols} skip={skip}: {err.max():.3e}"
+    return g, feeds
+
+
+@pytest.mark.parametrize("variant", [name for name, _ in ROW_VARIANTS])
+@pytest.mark.parametrize("skip", [False, True])
+def test_layer_norm_fp16(tmp_path, variant, skip):
+    """Every row-group variant over rows at each variant's register limit,
+    ragged row counts, rows past every limit and unaligned column counts."""
+    rng = np.random.default_rng(17)
+    kid = "skip_layer_norm.fp16.last_axis" if skip else "layer_norm.fp16.last_axis"
+    pack = filtered_pack(tmp_path / "pack", only_variant(kid, variant))
+    opts = engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled")
+    for rows, cols in ((512, 768), (17, 100), (4, 5000), (64, 1024), (33, 128), (9, 256), (3, 4096), (5, 40)):
+        g, feeds = layer_norm_graph(rng, rows, cols, skip)
+        out, eng, _ = run_graph(g, feeds, opts)
+        ops = eng.ops()
+        assert [op.op_type for op in ops] == (["SkipLayerNormalization"] if skip else ["LayerNormalization"])
+        assert ops[0].candidates[ops[0].selected_candidate].endswith(f"{kid}:{variant}")
+        err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, feeds)["y"])
+        assert err.max() <= 1e-2, f"{kid}:{variant} {rows}x{cols}: {err.max():.3e}"
 
 
 @pytest.mark.parametrize("op", ["Gelu", "Add"])

@@ -164,6 +164,30 @@ def test_layer_norm_two_pass_vs_torch():
     assert not np.allclose(got, want_skip, atol=1e-3)
 
 
+def test_softmax_last_axis():
+    from scipy.special import softmax as scipy_softmax
+
+    g = rng(8)
+    x = g.uniform(-50, 50, (5, 37))
+    got = oracle.softmax(x)
+    np.testing.assert_allclose(got, torch.softmax(torch.from_numpy(x), dim=-1).numpy(), rtol=1e-12, atol=1e-300)
+    np.testing.assert_allclose(got, scipy_softmax(x, axis=-1), rtol=1e-12, atol=1e-300)
+    # Invariants: rows sum to one; a per-row shift changes nothing.
+    np.testing.assert_allclose(got.sum(axis=-1), 1.0, rtol=1e-14)
+    np.testing.assert_allclose(oracle.softmax(x + g.uniform(-5, 5, (5, 1))), got, rtol=1e-12, atol=1e-300)
+    # Closed form: two entries give the logistic function of their difference,
+    # also where exp alone would overflow (the row max is subtracted first).
+    for a, b in ((0.3, -1.2), (1000.0, 1000.0 - math.log(2.0)), (-700.0, -705.0)):
+        want = [1.0 / (1.0 + math.exp(b - a)), 1.0 / (1.0 + math.exp(a - b))]
+        np.testing.assert_allclose(oracle.softmax(np.array([[a, b]])), [want], rtol=1e-14)
+    # -inf entries get 0; a row of -inf gives NaN, as in the reference.
+    masked = oracle.softmax(np.array([[0.0, -np.inf, 0.0], [-np.inf, -np.inf, -np.inf]]))
+    np.testing.assert_allclose(masked[0], [0.5, 0.0, 0.5], rtol=1e-15)
+    assert np.isnan(masked[1]).all()
+    # Planted: the softmax over the other axis is caught.
+    assert not np.allclose(oracle.softmax(x.T).T, got, atol=1e-3)
+
+
 def test_stem_known_answer():
     """Reference stem KAT (tests/cpp/test_cuda.cpp:449-479): one-hot 7x7 weights,
     identity BatchNorm; the logits have a closed form."""
