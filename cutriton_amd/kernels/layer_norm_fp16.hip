@@ -9,11 +9,13 @@
 // Unlike the reference (one 1024-wide block per row) any column count works.
 // A group of GROUP lanes owns one row (64 / GROUP rows per wavefront); each
 // lane keeps CHUNKS 16-byte chunks of the row in registers between the two
-// passes, so x (and the residual) are read once. Rows longer than
-// GROUP * 8 * CHUNKS columns, or not 16-byte aligned, are re-read from
-// global memory. Variants differ only in GROUP and CHUNKS: fewer chunks use
-// fewer registers and keep more rows in flight. Argument order is the pack
-// ABI of transformer.py:323-371.
+// passes, so x (and the residual) are read once. Longer aligned rows take
+// one statistics pass that merges per-chunk (count, mean, M2) triples
+// (Chan et al.'s pairwise variance update, as stable as two passes) and a
+// second pass that writes; unaligned rows take three element-wise passes.
+// Variants differ only in GROUP and CHUNKS: fewer chunks use fewer
+// registers and keep more rows in flight. Argument order is the pack ABI of
+// transformer.py:323-371.
 #include "common.h"
 
 namespace {
@@ -25,6 +27,31 @@ template <int GROUP>
 __device__ __forceinline__ float GroupSum(float v) {
 #pragma unroll
   for (int offset = GROUP / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+// Running statistics of a set of values: count, mean, sum of squared
+// deviations from the mean.
+struct Moments {
+  float n, mean, m2;
+};
+
+// Chan, Golub and LeVeque's update for the union of two disjoint sets.
+__device__ __forceinline__ Moments Merge(Moments a, Moments b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float delta = b.mean - a.mean;
+  const float wb = b.n / n;
+  return {n, a.mean + delta * wb, a.m2 + b.m2 + delta * delta * a.n * wb};
+}
+
+template <int GROUP>
+__device__ __forceinline__ Moments GroupMerge(Moments v) {
+#pragma unroll
+  for (int offset = GROUP / 2; offset > 0; offset >>= 1) {
+    const Moments other{__shfl_xor(v.n, offset, 64), __shfl_xor(v.mean, offset, 64), __shfl_xor(v.m2, offset, 64)};
+    v = Merge(v, other);
+  }
   return v;
 }
 
@@ -99,7 +126,51 @@ __device__ __forceinline__ void LayerNormRow(const _Float16* __restrict__ x, con
     return;
   }
 
-  // General path: element-strided, three passes over global memory.
+  const bool aligned = (columns % kChunk) == 0 &&
+                       ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(output) |
+                         reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta) |
+                         (SKIP ? reinterpret_cast<uintptr_t>(residual) : 0)) & 15) == 0;
+  auto load = [&](int col, float (&v)[kChunk]) {
+    const ct::f16x8 a = *reinterpret_cast<const ct::f16x8*>(xr + col);
+    ct::f16x8 b;
+    if (SKIP) b = *reinterpret_cast<const ct::f16x8*>(rr + col);
+#pragma unroll
+    for (int e = 0; e < kChunk; ++e) v[e] = static_cast<float>(a[e]) + (SKIP ? static_cast<float>(b[e]) : 0.0f);
+  };
+  if (aligned) {
+    // Long rows: statistics in one pass over 16-byte chunks, then the write.
+    Moments acc{0.0f, 0.0f, 0.0f};
+    for (int col = sub * kChunk; col < columns; col += GROUP * kChunk) {
+      float v[kChunk];
+      load(col, v);
+      float chunk_sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kChunk; ++e) chunk_sum += v[e];
+      const float chunk_mean = chunk_sum * (1.0f / kChunk);
+      float chunk_m2 = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kChunk; ++e) chunk_m2 += (v[e] - chunk_mean) * (v[e] - chunk_mean);
+      acc = Merge(acc, Moments{static_cast<float>(kChunk), chunk_mean, chunk_m2});
+    }
+    const Moments row_moments = GroupMerge<GROUP>(acc);
+    const float mean = row_moments.mean;
+    const float rstd = rsqrtf(row_moments.m2 * inv_columns + epsilon);
+    for (int col = sub * kChunk; col < columns; col += GROUP * kChunk) {
+      float v[kChunk];
+      load(col, v);
+      const ct::f16x8 g = *reinterpret_cast<const ct::f16x8*>(gamma + col);
+      const ct::f16x8 bt = *reinterpret_cast<const ct::f16x8*>(beta + col);
+      ct::f16x8 y;
+#pragma unroll
+      for (int e = 0; e < kChunk; ++e) {
+        y[e] = static_cast<_Float16>((v[e] - mean) * rstd * static_cast<float>(g[e]) + static_cast<float>(bt[e]));
+      }
+      *reinterpret_cast<ct::f16x8*>(yr + col) = y;
+    }
+    return;
+  }
+
+  // Unaligned rows: element-strided, three passes over global memory.
   auto value = [&](int col) {
     return static_cast<float>(xr[col]) + (SKIP ? static_cast<float>(rr[col]) : 0.0f);
   };

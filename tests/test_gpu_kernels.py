@@ -419,6 +419,19 @@ def test_layer_norm_fp16(tmp_path, variant, skip):
         assert err.max() <= 1e-2, f"{kid}:{variant} {rows}x{cols}: {err.max():.3e}"
 
 
+@pytest.mark.parametrize("skip", [False, True])
+def test_layer_norm_long_rows_with_a_large_mean(skip):
+    """Rows past every register limit (the one-pass merged statistics) with a
+    mean far from zero, where a sum-of-squares variance would lose digits."""
+    rng = np.random.default_rng(19)
+    for rows, cols in ((3, 12288), (5, 4104)):
+        g, feeds = layer_norm_graph(rng, rows, cols, skip)
+        feeds["x"] = (feeds["x"].astype(np.float32) * 3 + 40).astype(np.float16)
+        out, _, _ = run_graph(g, feeds)
+        err = np.abs(out["y"].astype(np.float64) - oracle.evaluate(g, feeds)["y"])
+        assert err.max() <= 1e-2, f"{rows}x{cols} skip={skip}: {err.max():.3e}"
+
+
 @pytest.mark.parametrize("op", ["Gelu", "Add"])
 @pytest.mark.parametrize("count", [(512, 3072), (3, 37)])
 def test_fp16_elementwise_kernels(op, count):
