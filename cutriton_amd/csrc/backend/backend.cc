@@ -92,7 +92,7 @@ bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const Val
     if (!layout_ok(name)) return false;
   }
   // An input read in another layout must be a constant (the engine re-lays
-  // it out once, at constant upload): rank-4 FP32 for OHWI, rank 2 for NK.
+  // it out once, at constant upload): rank-4 FP32 for OHWI, rank 2 for NK and T.
   for (const auto& argument : artifact.arguments) {
     const KernelArgumentSource& s = argument.source;
     if (s.layout.empty()) continue;
@@ -100,7 +100,7 @@ bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const Val
     const ValueDesc* v = lookup(node.inputs()[static_cast<std::size_t>(s.index)]);
     if (v == nullptr || !v->is_constant) return false;
     const bool ohwi = s.layout == "OHWI" && v->tensor.shape.size() == 4 && v->tensor.dtype == DataType::kFloat32;
-    const bool nk = s.layout == "NK" && v->tensor.shape.size() == 2;
+    const bool nk = (s.layout == "NK" || s.layout == "T") && v->tensor.shape.size() == 2;
     if (!ohwi && !nk) return false;
   }
   for (const auto& c : artifact.constraints) {

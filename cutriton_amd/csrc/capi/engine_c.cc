@@ -87,6 +87,37 @@ const char* ct_version(void) { return "cutriton-amd 0.1.0 (hip_gfx950)"; }
 ct_model* ct_model_create(void) { return new ct_model(); }
 void ct_model_destroy(ct_model* model) { delete model; }
 
+static int ImportOnnx(const void* data, size_t bytes, const char* path, const char* const* dim_names,
+                      const int64_t* dim_values, int dim_count, ct_model** model) {
+  if (model == nullptr || dim_count < 0 || (dim_count > 0 && (dim_names == nullptr || dim_values == nullptr))) {
+    return Invalid("ONNX import arguments are invalid");
+  }
+  *model = nullptr;
+  OnnxDimValues dims;
+  for (int i = 0; i < dim_count; ++i) {
+    if (dim_names[i] == nullptr) return Invalid("symbolic dimension name is null");
+    dims[dim_names[i]] = dim_values[i];
+  }
+  auto created = std::make_unique<ct_model>();
+  const Status status = path != nullptr ? ImportOnnxFile(path, dims, &created->model)
+                                        : ImportOnnxModel(data, bytes, dims, &created->model);
+  if (!status.ok()) return Report(status);
+  *model = created.release();
+  return 0;
+}
+
+int ct_model_import_onnx(const char* path, const char* const* dim_names, const int64_t* dim_values,
+                         int dim_count, ct_model** model) {
+  if (path == nullptr) return Invalid("ONNX path is null");
+  return ImportOnnx(nullptr, 0, path, dim_names, dim_values, dim_count, model);
+}
+
+int ct_model_import_onnx_buffer(const void* data, size_t bytes, const char* const* dim_names,
+                                const int64_t* dim_values, int dim_count, ct_model** model) {
+  if (data == nullptr && bytes != 0) return Invalid("ONNX buffer is null");
+  return ImportOnnx(data, bytes, nullptr, dim_names, dim_values, dim_count, model);
+}
+
 int ct_model_add_input(ct_model* model, const char* name, const int64_t* shape, int rank, int dtype,
                        const char* layout) {
   if (model == nullptr || name == nullptr) return Invalid("model or name is null");

@@ -82,7 +82,7 @@ Status RelayoutOnDevice(const std::string& layout, const TensorDesc& desc, const
     void* params[] = {&in, &out, &k, &c, &rs};
     return Launch(kernels->ohwi_b32, k * c * rs, params);
   }
-  if (layout == "NK") {
+  if (layout == "NK" || layout == "T") {
     if (desc.shape.size() != 2) return Status::InvalidArgument("NK needs a rank-2 tensor");
     int index = -1;
     switch (ElementSize(desc.dtype)) {

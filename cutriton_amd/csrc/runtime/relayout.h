@@ -14,7 +14,7 @@ namespace cutriton {
 // to `destination` (desc.ByteSize() bytes). The caller synchronizes the
 // device before reading `destination`.
 //   "OHWI": rank-4 4-byte elements, [K][C][R][S] -> [K][R][S][C];
-//   "NK":   rank-2 1/2/4/8-byte elements, [K][N] -> [N][K].
+//   "NK", "T": rank-2 1/2/4/8-byte elements, [R][C] -> [C][R].
 Status RelayoutOnDevice(const std::string& layout, const TensorDesc& desc, const void* source, void* destination,
                         int device);
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Any, Sequence
 
 import numpy as np
@@ -65,6 +66,8 @@ def _lib() -> ctypes.CDLL:
         "ct_model_set_attr_bool": (I, [P, C, C, I]),
         "ct_model_set_attr_string": (I, [P, C, C, C]),
         "ct_model_run_default_passes": (I, [P, I, I]),
+        "ct_model_import_onnx": (I, [C, ctypes.POINTER(C), c_int64_p, I, ctypes.POINTER(P)]),
+        "ct_model_import_onnx_buffer": (I, [P, S, ctypes.POINTER(C), c_int64_p, I, ctypes.POINTER(P)]),
         "ct_model_node_count": (I, [P]),
         "ct_model_node_op_type": (I, [P, I, C, S]),
         "ct_options_create": (P, []),
@@ -107,7 +110,7 @@ def _lib() -> ctypes.CDLL:
 
 def _check(code: int) -> None:
     if code != 0:
-        raise CutritonError(code, _lib().ct_last_error().decode())
+        raise CutritonError(code, _lib().ct_last_error().decode(errors="replace"))
 
 
 def _shape(dims: Sequence[int]) -> tuple[Any, int]:
@@ -134,6 +137,26 @@ class Model:
         if getattr(self, "handle", None):
             self._lib.ct_model_destroy(self.handle)
             self.handle = None
+
+    @classmethod
+    def from_onnx(cls, source: str | bytes | Path, dim_values: dict[str, int] | None = None) -> "Model":
+        """Imports an ONNX model (a file path or the serialized bytes);
+        `dim_values` sizes the symbolic input dimensions by name."""
+        lib = _lib()
+        names = list((dim_values or {}).keys())
+        c_names = (ctypes.c_char_p * max(1, len(names)))(*[_b(n) for n in names])
+        c_values = (ctypes.c_int64 * max(1, len(names)))(*[int((dim_values or {})[n]) for n in names])
+        handle = ctypes.c_void_p()
+        if isinstance(source, (bytes, bytearray)):
+            data = bytes(source)
+            _check(lib.ct_model_import_onnx_buffer(data, len(data), c_names, c_values, len(names),
+                                                   ctypes.byref(handle)))
+        else:
+            _check(lib.ct_model_import_onnx(_b(str(source)), c_names, c_values, len(names), ctypes.byref(handle)))
+        model = cls.__new__(cls)
+        model._lib = lib
+        model.handle = handle.value
+        return model
 
     def add_input(self, name: str, shape: Sequence[int], dtype: str = "float32", layout: str = "NCHW") -> None:
         dims, rank = _shape(shape)

@@ -23,7 +23,7 @@ from typing import Any
 # An input may ask for another layout of a constant of the same logical shape:
 # OHWI stores an OIHW convolution weight as [out][kh][kw][in]; NK stores a
 # [K, N] matrix transposed, as [N][K].
-INPUT_LAYOUTS = frozenset({"OHWI", "NK"})
+INPUT_LAYOUTS = frozenset({"OHWI", "NK", "T"})
 
 ARGUMENT_SOURCES: dict[str, frozenset[str]] = {
     "input": frozenset({"kind", "index", "layout"}),

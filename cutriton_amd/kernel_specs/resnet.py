@@ -182,27 +182,37 @@ def register_gemm() -> None:
     # C[M,N] = A[M,K] B[K,N]: x = ceil(N / BLOCK_N), y = ceil(M / BLOCK_M).
     grid = (ceil_div(output_dim(1), meta("BLOCK_N")), ceil_div(output_dim(0), meta("BLOCK_M")))
     tiles = (("m64n64", 64, 64, 32), ("m128n128", 128, 128, 32))
-    dims = (
-        arg("m", "i32", "input_dim", index=0, axis=0),
-        arg("n", "i32", "input_dim", index=1, axis=1),
-        arg("k", "i32", "input_dim", index=0, axis=1),
-    )
-    common = (
-        {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
-        {"kind": "attribute_i64_eq", "name": "transB", "value": 0, "default": 0},
-        {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
-        {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
-    )
     # Split-K: z = SPLIT workgroups per output tile, runtime scratch as for
     # the split-K convolutions.
     split_tiles = (("m64n64s8", 64, 64, 32, 8), ("m64n64s16", 64, 64, 32, 16))
     split_grid = grid + (meta("SPLIT"),)
+    # transB = 1 (e.g. an exported Linear layer: B is [N][K]): the kernels
+    # read B's transposed copy ("T" layout, made at constant upload), which
+    # is the [K][N] order they take for transB = 0.
+    for trans_b, suffix in ((0, ""), (1, "_tb")):
+        common = (
+            {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
+            {"kind": "attribute_i64_eq", "name": "transB", "value": trans_b, "default": 0},
+            {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+            {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
+        )
+        dims = (
+            arg("m", "i32", "input_dim", index=0, axis=0),
+            arg("n", "i32", "input_dim", index=1, axis=trans_b ^ 1),
+            arg("k", "i32", "input_dim", index=0, axis=1),
+        )
+        register_gemm_family(suffix, {"layout": "T"} if trans_b else {}, common, dims, grid, tiles, split_tiles,
+                             split_grid)
+
+
+def register_gemm_family(suffix, b_source, common, dims, grid, tiles, split_tiles, split_grid) -> None:
     for kernel_id, prefix, inputs, extra in (
         ("gemm.fp32.mfma", "gemm_fp32", ("a", "b"), ()),
         ("gemm_bias.fp32.mfma", "gemm_bias_fp32", ("a", "b", "bias"),
          ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)),
     ):
-        arguments = tuple(arg(name, "*fp32", "input", index=i) for i, name in enumerate(inputs)) + (
+        arguments = tuple(arg(name, "*fp32", "input", index=i, **(b_source if name == "b" else {}))
+                          for i, name in enumerate(inputs)) + (
             arg("output", "*fp32", "output", index=0),
         ) + dims + reserved()
         variants = tuple(
@@ -211,7 +221,7 @@ def register_gemm() -> None:
             for name, bm, bn, bk in tiles
         )
         register(KernelSpec(
-            kernel_id, "Gemm", 1, CONV_SOURCE, arguments, grid, variants,
+            kernel_id + suffix, "Gemm", 1, CONV_SOURCE, arguments, grid, variants,
             constraints=({"kind": "input_count_eq", "value": len(inputs)},) + common + extra,
         ))
         split_variants_ = tuple(
@@ -221,7 +231,8 @@ def register_gemm() -> None:
             for name, bm, bn, bk, split in split_tiles
         )
         register(KernelSpec(
-            kernel_id.replace(".mfma", ".splitk"), "Gemm", 1, CONV_SOURCE, arguments, split_grid, split_variants_,
+            kernel_id.replace(".mfma", ".splitk") + suffix, "Gemm", 1, CONV_SOURCE, arguments, split_grid,
+            split_variants_,
             constraints=({"kind": "input_count_eq", "value": len(inputs)},) + common + extra,
         ))
 

@@ -43,12 +43,13 @@ GEMM_DIMS = (
     arg("k", "i32", "input_dim", index=0, axis=1),
 )
 
-GEMM_CONSTRAINTS = (
-    {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
-    {"kind": "attribute_i64_eq", "name": "transB", "value": 0, "default": 0},
-    {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
-    {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
-)
+def gemm_constraints(trans_b: int) -> tuple[dict, ...]:
+    return (
+        {"kind": "attribute_i64_eq", "name": "transA", "value": 0, "default": 0},
+        {"kind": "attribute_i64_eq", "name": "transB", "value": trans_b, "default": 0},
+        {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
+        {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
+    )
 
 
 # Weight-transposed kernels (gemm_fp16_nt.hip): `b` is bound to the [N][K]
@@ -100,16 +101,20 @@ def register_gemms() -> None:
         ("gemm_gelu_bias.fp16.mfma", "GemmGelu", "gemm_gelu_bias_fp16", True),
     ):
         inputs = ("a", "b", "bias") if bias else ("a", "b")
-        constraints = ({"kind": "input_count_eq", "value": len(inputs)},) + GEMM_CONSTRAINTS
-        if bias:
-            constraints += ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)
         # The weight-transposed family comes first in the pack (kernel ids sort
         # that way), so its default is the untuned choice whenever B is a
         # constant; "_kn" kernels read B as it is and serve every other Gemm.
-        for suffix, source, variants, b_source in (
-            ("", GEMM_NT_SOURCE, gemm_nt_variants(prefix.replace("_fp16", "_nt_fp16")), {"layout": "NK"}),
-            ("_kn", GEMM_SOURCE, gemm_variants(prefix), {}),
+        # With transB = 1 (an exported Linear layer) B is [N][K] already and
+        # the "_tb" entries pass it to the same NT kernels as it is.
+        nt_variants = gemm_nt_variants(prefix.replace("_fp16", "_nt_fp16"))
+        for suffix, source, variants, b_source, trans_b in (
+            ("", GEMM_NT_SOURCE, nt_variants, {"layout": "NK"}, 0),
+            ("_kn", GEMM_SOURCE, gemm_variants(prefix), {}, 0),
+            ("_tb", GEMM_NT_SOURCE, nt_variants, {}, 1),
         ):
+            constraints = ({"kind": "input_count_eq", "value": len(inputs)},) + gemm_constraints(trans_b)
+            if bias:
+                constraints += ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)
             arguments = tuple(
                 arg(name, "*fp16", "input", index=i, **(b_source if name == "b" else {}))
                 for i, name in enumerate(inputs)

@@ -43,16 +43,21 @@ struct KernelArgumentSource {
   int64_t default_int{0};
   double default_float{0.0};
   // "input" only: the kernel reads this input in another memory layout of
-  // the same logical shape. Two layouts are defined:
+  // the same logical shape. Three layouts are defined:
   //   "OHWI": a rank-4 FP32 OIHW weight stored as [out][kh][kw][in];
-  //   "NK":   a rank-2 [K][N] matrix stored transposed, as [N][K].
+  //   "NK":   a rank-2 [K][N] GEMM weight stored transposed, as [N][K];
+  //   "T":    any rank-2 constant stored transposed (the same copy as "NK",
+  //           named for a weight that is [N][K] already, e.g. a Gemm with
+  //           transB = 1, read by a kernel that wants [K][N]).
   // The input must be a constant; the engine keeps the re-laid-out copy
   // beside the original.
   std::string layout;
 };
 
 // The layouts an input argument may request.
-inline bool IsInputLayout(const std::string& layout) { return layout == "OHWI" || layout == "NK"; }
+inline bool IsInputLayout(const std::string& layout) {
+  return layout == "OHWI" || layout == "NK" || layout == "T";
+}
 
 // Name of the re-laid-out copy of constant `name` in `layout`.
 inline std::string LaidOutConstantName(const std::string& name, const std::string& layout) {

@@ -62,6 +62,16 @@ int ct_model_set_attr_string(ct_model* model, const char* node, const char* key,
 /* Runs the default pass pipeline in place (fusion tests, inspection). */
 int ct_model_run_default_passes(ct_model* model, int transformer_fusions,
                                 int residual_epilogue_fusion);
+/* Reads an ONNX model into a new model (*model; free with
+ * ct_model_destroy). Symbolic input dimensions take the `dim_count` sizes
+ * named by `dim_names`. No counterpart in the reference, which has no
+ * importer (python/cutriton/api.py:77-99 only lists a model's structure
+ * through the onnx package); for callers that hold .onnx files. */
+int ct_model_import_onnx(const char* path, const char* const* dim_names, const int64_t* dim_values,
+                         int dim_count, ct_model** model);
+/* As ct_model_import_onnx, from `bytes` of a serialized ModelProto. */
+int ct_model_import_onnx_buffer(const void* data, size_t bytes, const char* const* dim_names,
+                                const int64_t* dim_values, int dim_count, ct_model** model);
 int ct_model_node_count(const ct_model* model);
 /* Copies node `index`'s op_type into `buffer` (truncated to `length`). */
 int ct_model_node_op_type(const ct_model* model, int index, char* buffer, size_t length);

@@ -14,20 +14,22 @@ from cutriton_amd import engine, workloads
 from cutriton_amd.native import PACK_DIR
 
 
-def run_graph(graph: workloads.GraphSpec, feeds: dict[str, np.ndarray], options: engine.CompileOptions | None = None,
+def run_model(model: engine.Model, feeds: dict[str, np.ndarray], outputs: Iterable[str],
+              input_layouts: dict[str, str], options: engine.CompileOptions | None = None,
               repeats: int = 1) -> tuple[dict[str, np.ndarray], engine.Engine, engine.ExecutionContext]:
-    """Builds, binds (device copies of `feeds`) and runs `graph`; returns host outputs."""
+    """Builds `model`, binds device copies of `feeds` and runs; returns host
+    outputs (rank-4 outputs bound NCHW), the engine and the context."""
     import torch
 
-    eng = engine.build_engine(workloads.to_model(graph), options or engine.CompileOptions(tuning_mode="disabled"))
+    eng = engine.build_engine(model, options or engine.CompileOptions(tuning_mode="disabled"))
     ctx = eng.create_execution_context()
     keep = []
     for name, value in feeds.items():
         t = torch.from_numpy(np.ascontiguousarray(value)).to("cuda:0")
         keep.append(t)
-        ctx.bind_input(name, t, layout=graph.inputs[name][2])
+        ctx.bind_input(name, t, layout=input_layouts[name])
     outs = {}
-    for name in graph.outputs:
+    for name in outputs:
         shape, dtype = eng.value_desc(name)
         t = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
         outs[name] = t
@@ -35,6 +37,13 @@ def run_graph(graph: workloads.GraphSpec, feeds: dict[str, np.ndarray], options:
     for _ in range(repeats):
         ctx.run()
     return {k: v.cpu().numpy() for k, v in outs.items()}, eng, ctx
+
+
+def run_graph(graph: workloads.GraphSpec, feeds: dict[str, np.ndarray], options: engine.CompileOptions | None = None,
+              repeats: int = 1) -> tuple[dict[str, np.ndarray], engine.Engine, engine.ExecutionContext]:
+    """Builds, binds (device copies of `feeds`) and runs `graph`; returns host outputs."""
+    layouts = {name: graph.inputs[name][2] for name in feeds}
+    return run_model(workloads.to_model(graph), feeds, graph.outputs, layouts, options, repeats)
 
 
 def filtered_pack(tmp: Path, keep: Any) -> str:

@@ -223,11 +223,15 @@ def test_tuner_runs_every_candidate(tmp_path):
                                             ("splitk", "m64n64s16")))
 @pytest.mark.parametrize("m,k,n,bias", [(32, 2048, 1000, False), (5, 37, 29, True), (130, 64, 70, False),
                                          (3, 2048, 1000, True)])
-def test_gemm_fp32(tmp_path, family, variant, m, k, n, bias):
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_gemm_fp32(tmp_path, family, variant, m, k, n, bias, trans_b):
+    """transB = 1 (B stored [N][K], as an exported Linear layer has it) runs
+    the "_tb" entries, which read B's transposed copy."""
     rng = np.random.default_rng(3)
     base = "gemm_bias.fp32" if bias else "gemm.fp32"
-    kid = f"{base}.{family}"
-    sibling = f"{base}.{'splitk' if family == 'mfma' else 'mfma'}"
+    suffix = "_tb" if trans_b else ""
+    kid = f"{base}.{family}{suffix}"
+    sibling = f"{base}.{'splitk' if family == 'mfma' else 'mfma'}{suffix}"
 
     def keep(e: dict) -> bool:
         return e["kernel_id"] != sibling and (e["kernel_id"] != kid or e["variant_id"] == variant)
@@ -235,14 +239,16 @@ def test_gemm_fp32(tmp_path, family, variant, m, k, n, bias):
     pack = filtered_pack(tmp_path / "pack", keep)
     g = workloads.GraphSpec()
     g.inputs["a"] = ((m, k), "float32", "")
-    g.constant("b", rng.normal(0, 0.05, (k, n)).astype(np.float32))
+    g.constant("b", rng.normal(0, 0.05, (n, k) if trans_b else (k, n)).astype(np.float32))
     ins = ["a", "b"]
     if bias:
         ins.append(g.constant("bias", rng.normal(0, 0.1, n).astype(np.float32)))
-    g.add("gemm", "Gemm", ins, ["y"])
+    g.add("gemm", "Gemm", ins, ["y"], **({"transB": 1} if trans_b else {}))
     g.outputs.append("y")
     feeds = {"a": rng.standard_normal((m, k), dtype=np.float32)}
-    out, _, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    op = eng.ops()[0]
+    assert op.candidates[op.selected_candidate].endswith(f"{kid}:{variant}")
     assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"gemm fp32 {variant} {m}x{k}x{n}")
 
 
@@ -278,14 +284,14 @@ def test_global_average_pool(shape):
     assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"gap {shape}")
 
 
-def gemm16_graph(rng, m, k, n, gelu, bias):
+def gemm16_graph(rng, m, k, n, gelu, bias, trans_b=False):
     g = workloads.GraphSpec()
     g.inputs["a"] = ((m, k), "float16", "")
-    g.constant("b", rng.normal(0, 0.05, (k, n)).astype(np.float16))
+    g.constant("b", rng.normal(0, 0.05, (n, k) if trans_b else (k, n)).astype(np.float16))
     ins = ["a", "b"]
     if bias:
         ins.append(g.constant("bias", rng.normal(0, 0.1, n).astype(np.float16)))
-    y = g.add("gemm", "Gemm", ins, ["h"])
+    y = g.add("gemm", "Gemm", ins, ["h"], **({"transB": 1} if trans_b else {}))
     if gelu:
         y = g.add("gelu", "Gelu", [y], ["y"])
     g.outputs.append(y)
@@ -294,8 +300,10 @@ def gemm16_graph(rng, m, k, n, gelu, bias):
 
 # Every tile variant runs the bias + GELU epilogue; every epilogue runs on
 # one variant of each family.
+# "_tb" (transB = 1, B stored [N][K]) runs the NT tiles on B as it is.
 GEMM16_CASES = [(f, v, True, True) for f, v in GEMM16_VARIANTS] + [
-    (f, v, gelu, bias) for f, v in (("", "m128n128w4"), ("_kn", "m128n128k64"))
+    ("_tb", v, True, True) for f, v in GEMM16_VARIANTS if f == ""] + [
+    (f, v, gelu, bias) for f, v in (("", "m128n128w4"), ("_kn", "m128n128k64"), ("_tb", "m128n128w4"))
     for gelu, bias in ((False, False), (True, False), (False, True))]
 
 
@@ -305,7 +313,9 @@ def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
     base = {(False, False): "gemm.fp16.mfma", (True, False): "gemm_gelu.fp16.mfma",
             (False, True): "gemm_bias.fp16.mfma", (True, True): "gemm_gelu_bias.fp16.mfma"}[(gelu, bias)]
     kid = base + family
-    sibling = base + ("_kn" if family == "" else "")
+    # The other family serving the same transB; none serves transB = 1.
+    sibling = {"": base + "_kn", "_kn": base, "_tb": None}[family]
+    trans_b = family == "_tb"
 
     def keep(e: dict) -> bool:
         if e["kernel_id"] == sibling:
@@ -317,7 +327,7 @@ def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
     # (the element-wise loader) and of the 64-deep tile.
     for m, k, n in ((512, 768, 3072), (17, 128, 40), (70, 72, 37), (300, 200, 264), (33, 100, 50), (1, 8, 4),
                     (260, 96, 520)):
-        g, feeds = gemm16_graph(rng, m, k, n, gelu, bias)
+        g, feeds = gemm16_graph(rng, m, k, n, gelu, bias, trans_b)
         out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
         ops = eng.ops()
         assert len(ops) == 1 and ops[0].candidates[ops[0].selected_candidate].endswith(f"{kid}:{variant}"), ops
