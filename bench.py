@@ -220,7 +220,7 @@ def bench_ffn(args, cache_dir: str) -> dict:
         / 1e12 / FP16_MFMA_PEAK_TFLOPS
     log(f"  ffn: {ms_per_step * 1e3:.1f} us/step; GemmGelu {out['gemm_gelu_us']:.1f} us "
         f"({out['gemm_gelu_tflops']:.0f} TF), Gemm {out['gemm_us']:.1f} us ({out['gemm_tflops']:.0f} TF), "
-        f"SkipLN {out['skip_layer_norm_us']:.1f} us")
+        f"SkipLN {out['skip_layer_norm_us']:.1f} us; selected {[s.rsplit(':', 1)[1] for s in selected]}")
     return out
 
 

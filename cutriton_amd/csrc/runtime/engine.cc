@@ -15,9 +15,12 @@
 //     candidates, LRU eviction of the least recently used graph (925-1079);
 //   * Synchronize: stream sync, then per-op durations into the Profiler
 //     (1081-1119).
-// One deliberate difference: before timing candidates, the tuner runs the
+// Two deliberate differences: before timing candidates, the tuner runs the
 // default candidate of every op once, so that intermediate inputs hold the
-// values of the current inputs rather than uninitialised workspace memory.
+// values of the current inputs rather than uninitialised workspace memory;
+// and each timed sample is a back-to-back batch of runs (about 0.2 ms),
+// not one run between synchronisations, whose launch and idle overheads
+// are as large as a short kernel.
 #include "cutriton/runtime/engine.h"
 
 #include <algorithm>
@@ -800,14 +803,30 @@ Status ExecutionContext::PrepareTuning() {
           continue;
         }
       }
-      std::vector<float> samples;
-      for (int it = 0; it < std::max(1, config.measurement_iterations); ++it) {
+      // A sample is `launches` back-to-back runs of the candidate between
+      // one event pair, enough to last about kSampleMs, so that launch
+      // overhead and the idle gap after each synchronisation weigh the
+      // same for every candidate; the sample's time per run enters the
+      // median. Candidates are safe to rerun: graph replay relies on it.
+      constexpr double kSampleMs = 0.2;
+      auto time_runs = [&](int launches, float* ms) -> Status {
         CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(start, stream), "hipEventRecord"));
-        for (auto& kernel : kernels) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
+        for (int r = 0; r < launches; ++r) {
+          for (auto& kernel : kernels) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
+        }
         CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(end, stream), "hipEventRecord"));
         CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_synchronize(end), "hipEventSynchronize"));
+        CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_elapsed_ms(ms, start, end), "hipEventElapsedTime"));
+        *ms /= static_cast<float>(launches);
+        return Status::OK();
+      };
+      float probe_ms = 0.0f;
+      CUTRITON_RETURN_IF_ERROR(time_runs(1, &probe_ms));
+      const int launches = static_cast<int>(std::clamp(std::ceil(kSampleMs / std::max(probe_ms, 1e-4f)), 1.0, 64.0));
+      std::vector<float> samples;
+      for (int it = 0; it < std::max(1, config.measurement_iterations); ++it) {
         float ms = 0.0f;
-        CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_elapsed_ms(&ms, start, end), "hipEventElapsedTime"));
+        CUTRITON_RETURN_IF_ERROR(time_runs(launches, &ms));
         samples.push_back(ms);
       }
       std::sort(samples.begin(), samples.end());

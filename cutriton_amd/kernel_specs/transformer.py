@@ -69,6 +69,7 @@ GEMM_NT_TILES = (
     ("m128n256w8", 128, 256, 64, 8),
     ("m128n128w8", 128, 128, 64, 8),
     ("m128n128k128w8", 128, 128, 128, 8),
+    ("m128n64w8", 128, 64, 64, 8),
 )
 GEMM_NT_DEFAULT = "m128n128w4"
 

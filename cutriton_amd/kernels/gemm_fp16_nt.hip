@@ -363,3 +363,4 @@ CT_DEFINE_GEMM_NT(m256n128w8, 256, 128, 64, 2, 4, 2)
 CT_DEFINE_GEMM_NT(m128n256w8, 128, 256, 64, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n128w8, 128, 128, 64, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n128k128w8, 128, 128, 128, 2, 2, 4)
+CT_DEFINE_GEMM_NT(m128n64w8, 128, 64, 64, 2, 4, 2)

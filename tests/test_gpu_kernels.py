@@ -29,7 +29,7 @@ CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64"
 # "_kn" reads B as it is.
 GEMM16_VARIANTS = tuple(("", v) for v in ("m256n256w4", "m256n256w8", "m256n128w4", "m128n256w4", "m128n128w4",
                                           "m128n128k128w4", "m64n128w4", "m64n64w4", "m256n128w8", "m128n256w8",
-                                          "m128n128w8", "m128n128k128w8")) + \
+                                          "m128n128w8", "m128n128k128w8", "m128n64w8")) + \
     tuple(("_kn", v) for v in ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64"))
 
 
