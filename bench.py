@@ -9,6 +9,7 @@ Workloads (synthetic seeded inputs, random-init weights of the named shapes):
   * FP16 Softmax over attention scores [16*16*1024, 1024] and a standalone
     FP16 LayerNorm of the same shape: reported as GB/s (HBM-bound) beside the
     main line.
+  * Fused FP16 attention [8, 16, 2048, 128], full and causal: TFLOP/s.
 
 Timing: the first run tunes every op (TuneOnMiss, cache in a temporary
 directory). Then W untimed warm-up steps and K timed steps bracketed by
@@ -68,7 +69,7 @@ def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str):
     for name in graph.outputs:
         shape, dtype = eng.value_desc(name)
         outputs[name] = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
-        ctx.bind_output(name, outputs[name], layout="NCHW" if len(shape) == 4 else "")
+        ctx.bind_output(name, outputs[name], layout=eng.value_layout(name))
     return eng, ctx, (inputs, outputs)
 
 
@@ -259,6 +260,36 @@ def bench_norms(args, cache_dir: str) -> dict:
     return out
 
 
+def bench_attention(args, cache_dir: str) -> dict:
+    """Fused attention, FP16 [batch 8, heads 16, sequence 2048, head dim 128],
+    without and with the causal mask. FLOPs: 4 B H Sq Sk D for the two
+    products (the causal mask needs about half, counted as the exact number
+    of unmasked query-key pairs)."""
+    import numpy as np
+
+    from cutriton_amd import workloads
+
+    b, h, s, d = 8, 16, 2048, 128
+    rng = np.random.default_rng(workloads.SEED)
+    feeds = {n: rng.standard_normal((b, h, s, d), dtype=np.float32).astype(np.float16) for n in ("q", "k", "v")}
+    out: dict = {"shape": [b, h, s, d]}
+    for causal in (False, True):
+        g = workloads.GraphSpec()
+        for n in feeds:
+            g.inputs[n] = ((b, h, s, d), "float16", "")
+        g.add("attention", "Attention", ["q", "k", "v"], ["o"], is_causal=int(causal))
+        g.outputs.append("o")
+        _, kernel_ms, _, _, _ = run_workload(g, feeds, args.steps, args.warmup, cache_dir)
+        pairs = s * (s + 1) // 2 if causal else s * s
+        flops = 4 * b * h * pairs * d
+        key = "causal" if causal else "full"
+        out[f"{key}_us"] = kernel_ms[0] * 1e3
+        out[f"{key}_tflops"] = flops / (kernel_ms[0] * 1e-3) / 1e12
+    log(f"  attention {b}x{h}x{s}x{d}: {out['full_us']:.1f} us ({out['full_tflops']:.0f} TF), "
+        f"causal {out['causal_us']:.1f} us ({out['causal_tflops']:.0f} TF)")
+    return out
+
+
 def bench_copy(args, cache_dir: str) -> dict:
     """One Relu over 64 Mi non-negative floats: the relu_fp32 kernel reads and
     writes exactly 256 MiB each. Its GB/s is the streaming reference for the
@@ -328,7 +359,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "norms", "copy"), default="all")
+    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "norms", "attention", "copy"), default="all")
     parser.add_argument("--tuning-cache", default="",
                         help="tuning cache folder to reuse (default: a fresh temporary folder, so every op is tuned)")
     parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
@@ -372,6 +403,13 @@ def main() -> int:
             result.update(value=round(n["softmax_gbps"], 1), unit="GB/s", dtype="fp16",
                           ms_per_step=round(n["softmax_us"] * 1e-3, 4),
                           config={"workload": "softmax_fp16_262144x1024", "parallelism": "single-gpu"})
+    if args.workload in ("all", "attention"):
+        a = bench_attention(args, cache_dir)
+        result["attention"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in a.items()}
+        if args.workload == "attention":
+            result.update(value=round(a["full_tflops"], 3), unit="TFLOP/s", dtype="fp16",
+                          ms_per_step=round(a["full_us"] * 1e-3, 4),
+                          config={"workload": "attention_fp16_b8_h16_s2048_d128", "parallelism": "single-gpu"})
     if args.workload == "copy":
         c = bench_copy(args, cache_dir)
         result.update(value=round(c["gbps"], 1), unit="GB/s", ms_per_step=round(c["ms_per_step"], 4),

@@ -319,6 +319,14 @@ int ct_engine_value_desc(const ct_engine* engine, const char* name, int64_t* sha
   return FillDesc(value->tensor, shape, rank, dtype);
 }
 
+int ct_engine_value_layout(const ct_engine* engine, const char* name, char* buffer, size_t length) {
+  if (engine == nullptr || name == nullptr) return Invalid("engine or name is null");
+  const ValueDesc* value = engine->engine->plan().graph().FindValue(name);
+  if (value == nullptr) return Report(Status::NotFound(std::string("value is not in the plan: ") + name));
+  CopyString(value->tensor.layout, buffer, length);
+  return 0;
+}
+
 size_t ct_engine_workspace_bytes(const ct_engine* engine) {
   return engine == nullptr ? 0 : engine->engine->plan().memory_plan().workspace_size_bytes;
 }

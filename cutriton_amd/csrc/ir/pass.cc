@@ -6,6 +6,7 @@
 #include "cutriton/ir/pass.h"
 
 #include <algorithm>
+#include <cmath>
 #include <unordered_set>
 
 #include "cutriton/ir/op_schema.h"
@@ -183,6 +184,44 @@ Status InferLayerNormalization(Graph* graph, const Node& node) {
     return Status::Unsupported("only last-axis LayerNormalization is supported");
   }
   return graph->SetValueDesc(node.outputs()[0], x->tensor);
+}
+
+// Attention (the ONNX operator's 4-D form): Q [B, H, Sq, D], K [B, H, Sk, D],
+// V [B, H, Sk, D] -> [B, H, Sq, D], attributes `scale` and `is_causal`. The
+// attention-mask and past key/value inputs, the 3-D form (q_num_heads /
+// kv_num_heads), softcap, the extra outputs and a value head dimension that
+// differs from the query's are refused. The reference has no attention.
+Status InferAttention(Graph* graph, const Node& node) {
+  if (node.inputs().size() != 3 || node.outputs().size() != 1) {
+    return Status::Unsupported("Attention takes Q, K and V and gives one output (no mask, past or present)");
+  }
+  for (const char* key : {"q_num_heads", "kv_num_heads"}) {
+    if (node.attributes().count(key) != 0) return Status::Unsupported("Attention: 3-D inputs (" + std::string(key) + ")");
+  }
+  if (const auto softcap = node.GetAttribute<double>("softcap"); softcap && *softcap != 0.0) {
+    return Status::Unsupported("Attention: softcap");
+  }
+  if (GetIntAttribute(node, "qk_matmul_output_mode", 0) != 0) {
+    return Status::Unsupported("Attention: qk_matmul_output_mode");
+  }
+  const ValueDesc* q = graph->FindValue(node.inputs()[0]);
+  const ValueDesc* k = graph->FindValue(node.inputs()[1]);
+  const ValueDesc* v = graph->FindValue(node.inputs()[2]);
+  if (q == nullptr || k == nullptr || v == nullptr || q->tensor.shape.size() != 4 || k->tensor.shape.size() != 4 ||
+      v->tensor.shape.size() != 4) {
+    return Status::ShapeError("Attention expects Q, K and V of rank 4 [batch, heads, sequence, head dimension]");
+  }
+  const auto& qs = q->tensor.shape;
+  const auto& ks = k->tensor.shape;
+  const auto& vs = v->tensor.shape;
+  if (q->tensor.dtype != k->tensor.dtype || q->tensor.dtype != v->tensor.dtype || qs[0] != ks[0] ||
+      qs[0] != vs[0] || qs[1] != ks[1] || qs[1] != vs[1] || qs[3] != ks[3] || ks[2] != vs[2]) {
+    return Status::ShapeError("Attention: Q, K and V disagree in type, batch, heads, keys or head dimension");
+  }
+  if (vs[3] != qs[3]) return Status::Unsupported("Attention: a value head dimension other than the query's");
+  TensorDesc out = q->tensor;
+  out.layout = "";
+  return graph->SetValueDesc(node.outputs()[0], out);
 }
 
 // Softmax over the last axis only: the reference's kernel ignores `axis`
@@ -485,6 +524,29 @@ class FlattenGemmNormalizationPass final : public GraphPass {
   }
 };
 
+// Attention's `scale` as a float attribute: ONNX's default 1 / sqrt(D) from
+// Q's head dimension when it is absent, a float when it was given as an
+// integer. Kernels then read one value.
+class AttentionScalePass final : public GraphPass {
+ public:
+  const char* name() const override { return "attention_scale"; }
+  Status Run(Graph* graph) const override {
+    for (auto& node : graph->mutable_nodes()) {
+      if (node.op_type() != "Attention") continue;
+      if (const auto given = node.GetAttribute<int64_t>("scale")) {
+        node.SetAttribute("scale", static_cast<double>(*given));
+      } else if (!node.GetAttribute<double>("scale")) {
+        const ValueDesc* q = node.inputs().empty() ? nullptr : graph->FindValue(node.inputs()[0]);
+        if (q == nullptr || q->tensor.shape.empty() || q->tensor.shape.back() <= 0) {
+          return Status::ShapeError("Attention " + node.name() + " needs a known head dimension for its scale");
+        }
+        node.SetAttribute("scale", 1.0 / std::sqrt(static_cast<double>(q->tensor.shape.back())));
+      }
+    }
+    return Status::OK();
+  }
+};
+
 class StaticShapeValidationPass final : public GraphPass {
  public:
   const char* name() const override { return "static_shape_validation"; }
@@ -520,6 +582,7 @@ Status RegisterBuiltinOpSchemas() {
     CUTRITON_RETURN_IF_ERROR(add(op, 1, 1, InferSameAsFirstInput));
   }
   CUTRITON_RETURN_IF_ERROR(add("Softmax", 1, 1, InferSoftmax));
+  CUTRITON_RETURN_IF_ERROR(add("Attention", 3, 3, InferAttention));
   CUTRITON_RETURN_IF_ERROR(add("LayerNormalization", 2, 3, InferLayerNormalization));
   CUTRITON_RETURN_IF_ERROR(add("Add", 2, 2, InferElementwiseBinary));
   CUTRITON_RETURN_IF_ERROR(add("AddRelu", 2, 2, InferElementwiseBinary));
@@ -570,6 +633,7 @@ std::unique_ptr<GraphPass> CreateSkipLayerNormalizationFusionPass() {
 std::unique_ptr<GraphPass> CreateFlattenGemmNormalizationPass() {
   return std::make_unique<FlattenGemmNormalizationPass>();
 }
+std::unique_ptr<GraphPass> CreateAttentionScalePass() { return std::make_unique<AttentionScalePass>(); }
 std::unique_ptr<GraphPass> CreateStaticShapeValidationPass() {
   return std::make_unique<StaticShapeValidationPass>();
 }
@@ -591,6 +655,7 @@ PassManager CreateDefaultCompilePasses(bool enable_transformer_fusions,
   manager.Add(CreateTopologicalSortPass());
   manager.Add(CreateShapeInferencePass());
   manager.Add(CreateFlattenGemmNormalizationPass());
+  manager.Add(CreateAttentionScalePass());
   manager.Add(CreateDeadNodeEliminationPass());
   manager.Add(CreateStaticShapeValidationPass());
   return manager;

@@ -81,6 +81,7 @@ def _lib() -> ctypes.CDLL:
         "ct_engine_op_info": (I, [P, I, C, S, C, S, ctypes.POINTER(I), ctypes.POINTER(I)]),
         "ct_engine_candidate_id": (I, [P, I, I, C, S]),
         "ct_engine_value_desc": (I, [P, C, c_int64_p, ctypes.POINTER(I), ctypes.POINTER(I)]),
+        "ct_engine_value_layout": (I, [P, C, C, S]),
         "ct_engine_workspace_bytes": (S, [P]),
         "ct_engine_create_context": (I, [P, ctypes.POINTER(P)]),
         "ct_context_destroy": (None, [P]),
@@ -300,6 +301,12 @@ class Engine:
         rank, dtype = ctypes.c_int(8), ctypes.c_int()
         _check(self._lib.ct_engine_value_desc(self.handle, _b(name), dims, ctypes.byref(rank), ctypes.byref(dtype)))
         return list(dims[: rank.value]), DTYPE_NAMES[dtype.value]
+
+    def value_layout(self, name: str) -> str:
+        """The layout a binding of value `name` must carry."""
+        buf = ctypes.create_string_buffer(32)
+        _check(self._lib.ct_engine_value_layout(self.handle, _b(name), buf, 32))
+        return buf.value.decode()
 
     def workspace_bytes(self) -> int:
         return self._lib.ct_engine_workspace_bytes(self.handle)

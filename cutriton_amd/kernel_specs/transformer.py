@@ -15,6 +15,7 @@ from cutriton_amd.kernel_sdk.spec import (
     KernelVariant,
     arg,
     ceil_div,
+    literal,
     meta,
     mul,
     numel_grid,
@@ -201,7 +202,44 @@ def register_softmax() -> None:
     ))
 
 
+# Attention variants by the largest head dimension they serve. The ids sort
+# so that the 64-wide kernel is the untuned choice whenever it applies.
+ATTENTION_VARIANTS = (("d064", 64), ("d128", 128))
+ATTENTION_QUERIES_PER_WORKGROUP = 128
+
+
+def register_attention() -> None:
+    arguments = (
+        arg("q", "*fp16", "input", index=0),
+        arg("k", "*fp16", "input", index=1),
+        arg("v", "*fp16", "input", index=2),
+        arg("output", "*fp16", "output", index=0),
+        arg("batch", "i32", "input_dim", index=0, axis=0),
+        arg("heads", "i32", "input_dim", index=0, axis=1),
+        arg("sq", "i32", "input_dim", index=0, axis=2),
+        arg("sk", "i32", "input_dim", index=1, axis=2),
+        arg("d", "i32", "input_dim", index=0, axis=3),
+        arg("scale", "fp32", "attribute_f64", name="scale", default=1.0),
+        arg("causal", "i32", "attribute_i64", name="is_causal", default=0),
+    ) + reserved()
+    grid = (ceil_div(output_dim(2), literal(ATTENTION_QUERIES_PER_WORKGROUP)), mul(output_dim(0), output_dim(1)))
+    for name, dmax in ATTENTION_VARIANTS:
+        register(KernelSpec(
+            f"attention.fp16.{name}", "Attention", 1, "attention_fp16.hip", arguments, grid,
+            (KernelVariant("w4", f"attention_fp16_d{dmax}", num_warps=4, default=True),),
+            dtype="float16",
+            constraints=(
+                {"kind": "input_count_eq", "value": 3},
+                {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 4},
+                {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 4},
+                {"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 4},
+                {"kind": "dim_le", "source": "input", "index": 0, "axis": 3, "value": dmax},
+            ),
+        ))
+
+
 register_gemms()
 register_elementwise()
 register_norms()
 register_softmax()
+register_attention()

@@ -47,6 +47,9 @@ std::unique_ptr<GraphPass> CreateGemmGeluFusionPass();
 // Add -> LayerNormalization becomes SkipLayerNormalization.
 std::unique_ptr<GraphPass> CreateSkipLayerNormalizationFusionPass();
 std::unique_ptr<GraphPass> CreateFlattenGemmNormalizationPass();
+// Attention's default scale 1 / sqrt(head dimension) (no counterpart in the
+// reference, which has no attention).
+std::unique_ptr<GraphPass> CreateAttentionScalePass();
 std::unique_ptr<GraphPass> CreateStaticShapeValidationPass();
 
 // The default pipeline. `enable_transformer_fusions` toggles GemmGelu and

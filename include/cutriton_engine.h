@@ -106,6 +106,9 @@ int ct_engine_candidate_id(const ct_engine* engine, int op_index, int candidate_
 /* Shape/dtype of a value in the compiled graph; *rank is in/out (capacity). */
 int ct_engine_value_desc(const ct_engine* engine, const char* name, int64_t* shape,
                          int* rank, int* dtype);
+/* Layout of a value in the compiled graph ("NCHW", "" ...), copied into
+ * `buffer` (truncated to `length`): the layout a binding of it must carry. */
+int ct_engine_value_layout(const ct_engine* engine, const char* name, char* buffer, size_t length);
 size_t ct_engine_workspace_bytes(const ct_engine* engine);
 int ct_engine_create_context(const ct_engine* engine, ct_context** context);
 

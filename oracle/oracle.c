@@ -17,11 +17,16 @@
  *                             two-pass mean / centred variance; eps inside sqrt)
  *   ct_oracle_softmax         transformer.py:180-190 (last axis; subtract the
  *                             row max, exp, divide by the sum)
+ *   ct_oracle_attention       no reference kernel: the ONNX Attention
+ *                             operator's definition (softmax(scale Q K^T) V,
+ *                             upper-left causal mask), built from the
+ *                             softmax above
  * Parity pins (closed forms, invariants, brute force, torch float64) are in
  * tests/test_oracle.py.
  */
 #include <math.h>
 #include <stddef.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -152,5 +157,36 @@ void ct_oracle_softmax(const double* x, long rows, long cols, double* out) {
     }
     for (long j = 0; j < cols; ++j) yr[j] /= sum;
   }
+}
+
+/* Attention over `heads` independent [s_q, d] x [s_k, d] problems:
+ * out[i] = sum_j softmax_j(scale * q[i] . k[j]) v[j], with `causal` keeping
+ * only keys j <= i (upper-left alignment, as the ONNX Attention operator
+ * and torch's scaled_dot_product_attention define is_causal). */
+void ct_oracle_attention(const double* q, const double* k, const double* v, long heads, long s_q, long s_k, long d,
+                         double scale, int causal, double* out) {
+  double* logits = (double*)malloc((size_t)(s_k > 0 ? s_k : 1) * sizeof(double));
+  double* weights = (double*)malloc((size_t)(s_k > 0 ? s_k : 1) * sizeof(double));
+  for (long h = 0; h < heads; ++h) {
+    const double* qh = q + (size_t)h * s_q * d;
+    const double* kh = k + (size_t)h * s_k * d;
+    const double* vh = v + (size_t)h * s_k * d;
+    double* oh = out + (size_t)h * s_q * d;
+    for (long i = 0; i < s_q; ++i) {
+      for (long j = 0; j < s_k; ++j) {
+        double dot = 0.0;
+        for (long e = 0; e < d; ++e) dot += qh[(size_t)i * d + e] * kh[(size_t)j * d + e];
+        logits[j] = (causal && j > i) ? -INFINITY : scale * dot;
+      }
+      ct_oracle_softmax(logits, 1, s_k, weights);
+      for (long e = 0; e < d; ++e) {
+        double acc = 0.0;
+        for (long j = 0; j < s_k; ++j) acc += weights[j] * vh[(size_t)j * d + e];
+        oh[(size_t)i * d + e] = acc;
+      }
+    }
+  }
+  free(logits);
+  free(weights);
 }
 

@@ -56,8 +56,10 @@ def _lib() -> ctypes.CDLL:
         lib.ct_oracle_gelu.argtypes = [D, L, D]
         lib.ct_oracle_layer_norm.argtypes = [D, D, L, L, D, D, ctypes.c_double, D]
         lib.ct_oracle_softmax.argtypes = [D, L, L, D]
+        lib.ct_oracle_attention.argtypes = [D, D, D, L, L, L, L, ctypes.c_double, ctypes.c_int, D]
         for fn in ("ct_oracle_conv2d", "ct_oracle_batch_norm", "ct_oracle_max_pool", "ct_oracle_global_avg_pool",
-                   "ct_oracle_gemm", "ct_oracle_gelu", "ct_oracle_layer_norm", "ct_oracle_softmax"):
+                   "ct_oracle_gemm", "ct_oracle_gelu", "ct_oracle_layer_norm", "ct_oracle_softmax",
+                   "ct_oracle_attention"):
             getattr(lib, fn).restype = None
         _LIB = lib
     return _LIB
@@ -156,6 +158,19 @@ def softmax(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None,
+              causal: bool = False) -> np.ndarray:
+    """Attention over [..., S, D] inputs; scale defaults to 1 / sqrt(D)."""
+    q, k, v = _d(q), _d(k), _d(v)
+    s_q, d = q.shape[-2:]
+    s_k = k.shape[-2]
+    heads = q.size // (s_q * d) if s_q * d else 0
+    out = np.empty(q.shape[:-1] + (v.shape[-1],))
+    scale = 1.0 / np.sqrt(d) if scale is None else scale
+    _lib().ct_oracle_attention(_p(q), _p(k), _p(v), heads, s_q, s_k, d, scale, int(causal), _p(out))
+    return out
+
+
 def _ints(attrs: Mapping[str, Any], key: str, default):
     value = attrs.get(key, default)
     return list(value) if isinstance(value, (list, tuple)) else value
@@ -207,6 +222,8 @@ def evaluate(graph: Any, feeds: Mapping[str, np.ndarray]) -> dict[str, np.ndarra
             y = layer_norm(ins[0], ins[1], ins[2], a.get("epsilon", 1e-5))
         elif op == "SkipLayerNormalization":
             y = layer_norm(ins[0], ins[2], ins[3], a.get("epsilon", 1e-5), residual=ins[1])
+        elif op == "Attention":
+            y = attention(ins[0], ins[1], ins[2], a.get("scale"), bool(a.get("is_causal", 0)))
         elif op == "Softmax":
             if a.get("axis", -1) not in (-1, ins[0].ndim - 1):
                 raise NotImplementedError("the oracle's Softmax is over the last axis")

@@ -18,7 +18,8 @@ def run_model(model: engine.Model, feeds: dict[str, np.ndarray], outputs: Iterab
               input_layouts: dict[str, str], options: engine.CompileOptions | None = None,
               repeats: int = 1) -> tuple[dict[str, np.ndarray], engine.Engine, engine.ExecutionContext]:
     """Builds `model`, binds device copies of `feeds` and runs; returns host
-    outputs (rank-4 outputs bound NCHW), the engine and the context."""
+    outputs (each bound in the layout the plan gives it), the engine and the
+    context."""
     import torch
 
     eng = engine.build_engine(model, options or engine.CompileOptions(tuning_mode="disabled"))
@@ -33,7 +34,7 @@ def run_model(model: engine.Model, feeds: dict[str, np.ndarray], outputs: Iterab
         shape, dtype = eng.value_desc(name)
         t = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
         outs[name] = t
-        ctx.bind_output(name, t, layout="NCHW" if len(shape) == 4 else "")
+        ctx.bind_output(name, t, layout=eng.value_layout(name))
     for _ in range(repeats):
         ctx.run()
     return {k: v.cpu().numpy() for k, v in outs.items()}, eng, ctx

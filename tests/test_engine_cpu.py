@@ -145,6 +145,40 @@ def test_softmax_over_another_axis_is_refused(gfx950):
     assert err.value.kind == "Unsupported"
 
 
+def attention_model(shapes, **attrs):
+    g = workloads.GraphSpec()
+    for name, shape in zip(("q", "k", "v", "mask"), shapes):
+        g.inputs[name] = (shape, "float16", "")
+    g.add("attention", "Attention", list(g.inputs), ["o"], **attrs)
+    g.outputs.append("o")
+    return workloads.to_model(g)
+
+
+def test_attention_plan(gfx950):
+    eng = engine.build_engine(attention_model([(2, 4, 100, 64), (2, 4, 70, 64), (2, 4, 70, 64)]),
+                              engine.CompileOptions())
+    assert eng.value_desc("o") == ([2, 4, 100, 64], "float16") and eng.value_layout("o") == ""
+    ops = eng.ops()
+    assert [op.op_type for op in ops] == ["Attention"]
+    assert [c.split(":")[1] for c in ops[0].candidates] == ["attention.fp16.d064", "attention.fp16.d128"]
+    assert ops[0].selected_candidate == 0
+    ops = engine.build_engine(attention_model([(1, 2, 8, 128)] * 3, is_causal=1), engine.CompileOptions()).ops()
+    assert [c.split(":")[1] for c in ops[0].candidates] == ["attention.fp16.d128"]
+
+
+@pytest.mark.parametrize("shapes,attrs,kind", [
+    ([(2, 8, 64)] * 3, {}, "ShapeError"),                                          # 3-D inputs
+    ([(1, 2, 8, 64), (1, 2, 8, 64), (1, 2, 8, 32)], {}, "Unsupported"),            # value head dimension
+    ([(1, 2, 8, 64), (1, 3, 8, 64), (1, 2, 8, 64)], {}, "ShapeError"),             # heads disagree
+    ([(1, 2, 8, 64)] * 3, {"softcap": 30.0}, "Unsupported"),
+    ([(1, 2, 8, 256)] * 3, {}, "Unsupported"),                                     # no kernel for D = 256
+])
+def test_attention_refusals(gfx950, shapes, attrs, kind):
+    with pytest.raises(engine.CutritonError) as err:
+        engine.build_engine(attention_model(shapes, **attrs), engine.CompileOptions())
+    assert err.value.kind == kind
+
+
 def test_shape_profiles_resolve_on_cpu(gfx950):
     graph = workloads.resnet50(1)
     opts = engine.CompileOptions(shape_profiles={"batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224),

@@ -188,6 +188,46 @@ def test_softmax_last_axis():
     assert not np.allclose(oracle.softmax(x.T).T, got, atol=1e-3)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("s_q,s_k", [(7, 7), (5, 11), (9, 4)])
+def test_attention_vs_torch_sdpa(causal, s_q, s_k):
+    """Against torch's float64 scaled_dot_product_attention (upper-left
+    causal mask), default and explicit scale."""
+    g = rng(10)
+    q, k, v = (g.standard_normal((2, 3, s, 16)) for s in (s_q, s_k, s_k))
+    tq, tk, tv = (torch.from_numpy(a) for a in (q, k, v))
+    want = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).numpy()
+    np.testing.assert_allclose(oracle.attention(q, k, v, causal=causal), want, rtol=1e-12, atol=1e-13)
+    want_scaled = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal, scale=0.3).numpy()
+    np.testing.assert_allclose(oracle.attention(q, k, v, 0.3, causal), want_scaled, rtol=1e-12, atol=1e-13)
+    # Planted: the bottom-right causal alignment or a dropped scale is caught.
+    if causal and s_q != s_k:
+        shift = s_k - s_q
+        mask = np.tril(np.ones((s_q, s_k), bool), k=shift)
+        bottom_right = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=torch.from_numpy(mask)).numpy()
+        assert not np.allclose(bottom_right, want, atol=1e-3)
+    assert not np.allclose(oracle.attention(q, k, v, 1.0, causal), want, atol=1e-3)
+
+
+def test_attention_closed_forms():
+    g = rng(11)
+    v = g.standard_normal((1, 1, 6, 4))
+    # Identical keys: uniform weights, the mean of the values (causal: of the
+    # values up to each query).
+    q = g.standard_normal((1, 1, 6, 4))
+    k = np.ones((1, 1, 6, 4))
+    np.testing.assert_allclose(oracle.attention(np.zeros_like(q), k, v)[0, 0], np.tile(v[0, 0].mean(0), (6, 1)),
+                               rtol=1e-13)
+    causal = oracle.attention(np.zeros_like(q), k, v, causal=True)[0, 0]
+    np.testing.assert_allclose(causal, np.cumsum(v[0, 0], 0) / np.arange(1, 7)[:, None], rtol=1e-13)
+    # One key far ahead of the others: its value row.
+    k = np.zeros((1, 1, 6, 4))
+    k[0, 0, 3, 0] = 1.0
+    q = np.zeros((1, 1, 2, 4))
+    q[..., 0] = 1000.0
+    np.testing.assert_allclose(oracle.attention(q, k, v, scale=1.0)[0, 0], np.tile(v[0, 0, 3], (2, 1)), rtol=1e-12)
+
+
 def test_stem_known_answer():
     """Reference stem KAT (tests/cpp/test_cuda.cpp:449-479): one-hot 7x7 weights,
     identity BatchNorm; the logits have a closed form."""
