@@ -254,22 +254,34 @@ __device__ __forceinline__ void AttentionCore(uint8_t* __restrict__ lds, const _
       }
     }
 
-    // Online softmax per query; P in FP16 as the MFMA operand.
+    // Online softmax per query; P in FP16 as the MFMA operand. A block that
+    // lies inside the keys and, with the causal mask, at or before this
+    // wavefront's first query needs no mask (a wavefront-uniform test).
+    const int last_key = (kb + 1) * kKeys - 1;
+    const bool needs_mask = last_key >= sk || (causal && last_key > q_wave);
     f16x8 pf[2][2];  // [key step j][query tile]
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int query = q_wave + 16 * qt + lane16;
       float x[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[t][r] = s_acc[t][qt][r] * scale_log2;
+      if (needs_mask) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kb * kKeys + 16 * t + 4 * g + r;
+            if (key >= sk || (causal && key > query)) x[t][r] = -INFINITY;
+          }
+      }
       float row_max = -INFINITY;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kb * kKeys + 16 * t + 4 * g + r;
-          const bool masked = key >= sk || (causal && key > query);
-          x[t][r] = masked ? -INFINITY : s_acc[t][qt][r] * scale_log2;
-          row_max = fmaxf(row_max, x[t][r]);
-        }
+        for (int r = 0; r < 4; ++r) row_max = fmaxf(row_max, x[t][r]);
       const float m_new = fmaxf(m_run[qt], GroupMax16(row_max));
       // A row with no unmasked key yet keeps m = -inf: its P is 0 and its
       // (zero) accumulator needs no rescale.
