@@ -89,6 +89,9 @@ SPLIT_TILES = (
     ("m128n128s8", 128, 128, 32, 8),
     ("m64n64s2", 64, 64, 32, 2),
     ("m64n64s4", 64, 64, 32, 4),
+    ("m64n64s3", 64, 64, 32, 3),
+    ("m64n64s5", 64, 64, 32, 5),
+    ("m64n64s6", 64, 64, 32, 6),
     ("m64n64k64s2", 64, 64, 64, 2),
 )
 SPLIT_DEFAULT = "m128n128s4"

@@ -704,6 +704,11 @@ CT_DEFINE_SPLIT_VARIANTS(m128n128s4, 128, 128, 32, 2, 2, 4)
 CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s2, 64, 64, 32, 2, 2, 2)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s4, 64, 64, 32, 2, 2, 4)
+// Split counts that are not powers of two fill the last round of
+// workgroups better for some tile counts (e.g. 200 tiles x 5 = 1000).
+CT_DEFINE_SPLIT_VARIANTS(m64n64s3, 64, 64, 32, 2, 2, 3)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s5, 64, 64, 32, 2, 2, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s6, 64, 64, 32, 2, 2, 6)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the

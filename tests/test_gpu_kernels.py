@@ -23,7 +23,8 @@ pytestmark = pytest.mark.gpu
 CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
                  "mfma:m64n64k16", "mfma:m64n128k16", "mfma:m128n64k16", "mfma:m64n64k64", "mfma:m32n128",
                  "splitk:m128n128s2", "splitk:m128n128s4", "splitk:m128n128s8",
-                 "splitk:m64n64s2", "splitk:m64n64s4", "splitk:m64n64k64s2",
+                 "splitk:m64n64s2", "splitk:m64n64s4", "splitk:m64n64s3", "splitk:m64n64s5",
+                 "splitk:m64n64s6", "splitk:m64n64k64s2",
                  "direct:d64n256", "direct:d64n64", "direct:d32n64")
 # (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
 # "_kn" reads B as it is.
@@ -140,7 +141,22 @@ def test_small_channel_conv_does_not_match_wide_inputs():
     assert not any(".smallc:" in cand for cand in ops[0].candidates), ops[0].candidates
 
 
-@pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8", "m64n64s4"])
+@pytest.mark.parametrize("channels,variant", [(8, "m64n64s5"), (32, "m64n64s6")])
+def test_split_k_with_empty_shares(tmp_path, channels, variant):
+    """Splits whose depth range is empty add zero: 8 channels x 3 x 3 = 3 depth
+    tiles of 32 over 5 splits (general gather), and 32 channels x 3 x 3 = 9
+    tiles over 6 splits of 2 (channel-run gather, the last split starts past
+    the last tap)."""
+    rng = np.random.default_rng(29)
+    kernel_id = "conv_bn_relu.fp32.nchw.splitk"
+    pack = filtered_pack(tmp_path / "pack", only_kernel_variant(kernel_id, variant, "conv_bn_relu.fp32.nchw"))
+    g, feeds = conv_graph(rng, 2, channels, 10, 10, 16, 3, 1, 1, 1, tail="relu")
+    out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    assert eng.ops()[0].candidates[eng.ops()[0].selected_candidate].endswith(f"{kernel_id}:{variant}")
+    assert_close_fp32(out[g.outputs[0]], oracle.evaluate(g, feeds)[g.outputs[0]], what=f"{variant}, C={channels}")
+
+
+@pytest.mark.parametrize("variant", ["m128n128s2", "m128n128s8", "m64n64s4", "m64n64s5"])
 def test_split_k_shares_follow_the_inputs(tmp_path, variant):
     """Split-K partial sums travel through the runtime scratch and the tile
     counters reset themselves: consecutive launches on one context with
