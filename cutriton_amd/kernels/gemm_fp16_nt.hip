@@ -39,7 +39,9 @@
 // the activation fragment as its column operand, so it produces the
 // transposed 16x16 tile: a lane holds one output row m (lane % 16) and the
 // four consecutive columns n = 4 * (lane / 16) + 0..3 in its four registers.
-// The epilogue therefore stores 8 contiguous bytes per lane and tile.
+// When n is a multiple of 8 the epilogue stages the FP16 tile in LDS and
+// stores whole 16-byte row chunks; otherwise it stores the 8 contiguous bytes
+// per lane and tile directly.
 #include "common.h"
 
 namespace {
@@ -283,6 +285,63 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
 
   // Epilogue: lane holds row m = m0 + wm + 16 i + lane16 and columns
   // n = n0 + wn + 16 t + 4 quarter + 0..3.
+  if ((n & 7) == 0) {
+    // Rows of 16-byte chunks: the finished FP16 tile is staged in the LDS
+    // ring (idle after the last depth tile; every load has landed) and
+    // leaves as whole 16-byte chunks, consecutive lanes along a row. Stored
+    // straight from the MFMA layout, each instruction would write 16 rows x
+    // 32 bytes; this way each writes 1 KiB in runs of whole rows, about
+    // twice the store rate for the 32 MiB output of a 4096 x 4096 tile grid.
+    //
+    // LDS tile: BM rows of CHN chunks; chunk c of row r sits at
+    // c ^ ((r / RSW) % SWM). The 16 lanes of a quarter write one 8-byte
+    // column half of 16 consecutive rows, and the swizzle spreads them over
+    // 16 distinct 16-byte bank groups (RSW rows share one 256-byte bank line
+    // when rows are shorter than 256 bytes).
+    constexpr int CHN = BN / 8;
+    constexpr int RSW = BN >= 128 ? 1 : 128 / BN;
+    constexpr int SWM = CHN < 16 ? CHN : 16;
+    constexpr int THREADS = 64 * WAVES;
+    static_assert(BM * BN * 2 <= S::kLdsChunks * 16, "output tile fits the LDS ring");
+    static_assert((BM * CHN) % THREADS == 0, "whole rounds of chunk stores");
+    __syncthreads();  // every wavefront is done reading the last depth tile
+    _Float16* tile_h = reinterpret_cast<_Float16*>(lds);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int lc = wn + t * 16 + 4 * quarter;
+      float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (BIAS) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bias4[e] = n0 + lc + e < n ? static_cast<float>(bias[n0 + lc + e]) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int lr = wm + i * 16 + lane16;
+        f16x4 out4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[t][i][e];
+          if (BIAS) v += bias4[e];
+          if (GELU) v = GeluErfAs(v);
+          out4[e] = static_cast<_Float16>(v);
+        }
+        const int pc = (lc >> 3) ^ ((lr / RSW) % SWM);
+        *reinterpret_cast<f16x4*>(tile_h + lr * BN + pc * 8 + (lc & 7)) = out4;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < BM * CHN / THREADS; ++it) {
+      const int idx = it * THREADS + tid;
+      const int lr = idx / CHN;
+      const int c = idx % CHN;
+      const int row = m0 + lr;
+      const int col = n0 + c * 8;
+      const u32x4 v = lds[lr * CHN + (c ^ ((lr / RSW) % SWM))];
+      if (row < m && col < n) *reinterpret_cast<u32x4*>(output + static_cast<size_t>(row) * n + col) = v;
+    }
+    return;
+  }
   const bool vec_out = (n & 3) == 0;
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
