@@ -309,11 +309,14 @@ def register_bandwidth_kernels() -> None:
         arg("h", "i32", "input_dim", index=0, axis=2),
         arg("w", "i32", "input_dim", index=0, axis=3),
     ) + reserved()
-    # One 64-plane wavefront per 64 (image, channel) pairs, 4 per workgroup.
+    # One wavefront per PLANES (image, channel) pairs, 4 per workgroup.
     register(KernelSpec(
         "global_average_pool.fp32.nchw", "GlobalAveragePool", 1, "pool_fp32.hip", gap_arguments,
-        (ceil_div(mul(output_dim(0), output_dim(1)), literal(256)),),
-        variants("global_average_pool_fp32_nchw"), layout="NCHW",
+        (ceil_div(mul(output_dim(0), output_dim(1)), meta("PLANES_PER_GROUP")),),
+        (KernelVariant("w4", "global_average_pool_fp32_nchw", num_warps=4, meta={"PLANES_PER_GROUP": 256},
+                       default=True),
+         KernelVariant("p16", "global_average_pool_fp32_nchw_p16", num_warps=4, meta={"PLANES_PER_GROUP": 64})),
+        layout="NCHW",
     ))
 
 

@@ -15,22 +15,23 @@ constexpr int kThreads = 256;
 
 }  // namespace
 
-// A workgroup takes one (image, channel) plane and a band of kBand output
+// A workgroup takes one (image, channel) plane and a band of BAND output
 // rows. The input rows the band's windows read are copied once into LDS (one
 // contiguous span, 16 bytes per lane), rows outside the image as -inf; each
 // output is then the max over its window read from LDS, kernel row outer,
 // kernel column inner, skipping columns outside the image. Grid:
-// planes * ceil(out_h / kBand). A band too tall for LDS (large strides or
-// dilations) reads its windows from global memory instead.
+// planes * ceil(out_h / BAND). A band too tall for LDS (large strides or
+// dilations) reads its windows from global memory instead. (Bands of 16 and
+// 28 rows were measured on the ResNet-50 stem pool and were no faster.)
 namespace {
-constexpr int kBand = 8;
-constexpr int kPoolLds = 4096;  // floats
-}  // namespace
 
-CT_KERNEL void __launch_bounds__(kThreads)
-    max_pool_fp32_nchw(const float* __restrict__ x, float* __restrict__ output, int n, int c, int h, int w,
-                       int out_h, int out_w, int kernel_h, int kernel_w, int stride_h, int stride_w, int pad_h,
-                       int pad_w, int dilation_h, int dilation_w, void*, void*) {
+template <int BAND, int LDS_FLOATS>
+__device__ __forceinline__ void MaxPoolBand(const float* __restrict__ x, float* __restrict__ output, int n, int c,
+                                            int h, int w, int out_h, int out_w, int kernel_h, int kernel_w,
+                                            int stride_h, int stride_w, int pad_h, int pad_w, int dilation_h,
+                                            int dilation_w) {
+  constexpr int kBand = BAND;
+  constexpr int kPoolLds = LDS_FLOATS;
   __shared__ __attribute__((aligned(16))) float tile[kPoolLds];
   const int bands = (out_h + kBand - 1) / kBand;
   const int plane = blockIdx.x / bands;
@@ -88,14 +89,32 @@ CT_KERNEL void __launch_bounds__(kThreads)
   }
 }
 
-// One wavefront reduces 64 consecutive (image, channel) planes. When a plane
-// holds at most 64 pixels the wave's 64 planes are one contiguous span: it is
-// copied coalesced into LDS and each lane then sums its own plane in
+}  // namespace
+
+#define CT_DEFINE_MAX_POOL(NAME, BAND, LDS_FLOATS)                                                          \
+  CT_KERNEL void __launch_bounds__(kThreads)                                                                \
+      NAME(const float* __restrict__ x, float* __restrict__ output, int n, int c, int h, int w, int out_h,   \
+           int out_w, int kernel_h, int kernel_w, int stride_h, int stride_w, int pad_h, int pad_w,          \
+           int dilation_h, int dilation_w, void*, void*) {                                                  \
+    MaxPoolBand<BAND, LDS_FLOATS>(x, output, n, c, h, w, out_h, out_w, kernel_h, kernel_w, stride_h,        \
+                                  stride_w, pad_h, pad_w, dilation_h, dilation_w);                          \
+  }
+
+// symbol, output rows per workgroup, LDS floats
+CT_DEFINE_MAX_POOL(max_pool_fp32_nchw, 8, 4096)
+
+// One wavefront reduces PLANES consecutive (image, channel) planes. When a
+// plane holds at most 64 pixels the wave's planes are one contiguous span: it
+// is copied coalesced into LDS and each lane then sums its own plane in
 // increasing pixel order. Larger planes are summed by one lane directly.
-CT_KERNEL void __launch_bounds__(kThreads)
-    global_average_pool_fp32_nchw(const float* __restrict__ x, float* __restrict__ output, int n, int c, int h,
-                                  int w, void*, void*) {
-  constexpr int kPlanes = 64;
+// Fewer planes per wavefront give more wavefronts for the same tensor (the
+// 7x7 planes of ResNet-50: 1024 wavefronts at 64 planes, one per SIMD).
+namespace {
+
+template <int PLANES>
+__device__ __forceinline__ void GlobalAveragePoolPlanes(const float* __restrict__ x, float* __restrict__ output,
+                                                        int n, int c, int h, int w) {
+  constexpr int kPlanes = PLANES;
   constexpr int kMaxSpan = 64;
   __shared__ float span[kThreads / 64][kPlanes * kMaxSpan];
   const int lane = threadIdx.x & 63;
@@ -118,3 +137,16 @@ CT_KERNEL void __launch_bounds__(kThreads)
     output[first + lane] = sum / static_cast<float>(spatial);
   }
 }
+
+}  // namespace
+
+#define CT_DEFINE_GAP(NAME, PLANES)                                                                      \
+  CT_KERNEL void __launch_bounds__(kThreads)                                                             \
+      NAME(const float* __restrict__ x, float* __restrict__ output, int n, int c, int h, int w, void*,     \
+           void*) {                                                                                      \
+    GlobalAveragePoolPlanes<PLANES>(x, output, n, c, h, w);                                              \
+  }
+
+// symbol, planes per wavefront
+CT_DEFINE_GAP(global_average_pool_fp32_nchw, 64)
+CT_DEFINE_GAP(global_average_pool_fp32_nchw_p16, 16)

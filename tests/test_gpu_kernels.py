@@ -288,15 +288,20 @@ def test_max_pool_bit_exact(shape, kernel, stride, pad):
     assert np.array_equal(out["y"].view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(2, 2048, 7, 7), (3, 5, 1, 1), (1, 3, 60, 61), (1, 300, 8, 8)])
-def test_global_average_pool(shape):
+@pytest.mark.parametrize("shape", [(2, 2048, 7, 7), (3, 5, 1, 1), (1, 3, 60, 61), (1, 300, 8, 8), (1, 70, 7, 7)])
+@pytest.mark.parametrize("variant", ["w4", "p16"])
+def test_global_average_pool(tmp_path, shape, variant):
     rng = np.random.default_rng(9)
     g = workloads.GraphSpec()
     g.inputs["x"] = (shape, "float32", "NCHW")
     g.add("gap", "GlobalAveragePool", ["x"], ["y"])
     g.outputs.append("y")
     feeds = {"x": rng.standard_normal(shape, dtype=np.float32)}
-    out, _, _ = run_graph(g, feeds)
+    kid = "global_average_pool.fp32.nchw"
+    pack = filtered_pack(tmp_path / "pack", lambda e: e["kernel_id"] != kid or e["variant_id"] == variant)
+    out, eng, _ = run_graph(g, feeds, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    op = eng.ops()[0]
+    assert op.candidates[op.selected_candidate].endswith(f"{kid}:{variant}"), op
     assert_close_fp32(out["y"], oracle.evaluate(g, feeds)["y"], what=f"gap {shape}")
 
 
