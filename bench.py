@@ -4,6 +4,8 @@ Workloads (synthetic seeded inputs, random-init weights of the named shapes):
   * ResNet-50 v1.5, FP32 NCHW, batch 32: one step = one inference of the
     batch through BuildEngine/ExecutionContext (53 fused conv nodes, MaxPool,
     GAP, Flatten view, Gemm), replayed as one hipGraph. `value` is img/s.
+    Batch 64 (the top of the reference's dynamic-batch profile) on its own
+    engine is reported beside it.
   * FP16 FFN block M=4096, H=1024, I=4096 (GemmGelu -> Gemm -> SkipLayerNorm):
     reported as TFLOP/s of its two GEMMs beside the main line.
   * FP16 Softmax over attention scores [16*16*1024, 1024] and a standalone
@@ -146,10 +148,9 @@ def measured_traffic() -> int | None:
     return None
 
 
-def bench_resnet(args, cache_dir: str) -> dict:
+def bench_resnet(args, cache_dir: str, batch: int = 32) -> dict:
     from cutriton_amd import workloads
 
-    batch = 32
     graph = workloads.resnet50(batch)
     x = workloads.resnet50_input(batch)
     ms_per_step, kernel_ms, event_ms, ops, selected = run_workload(graph, {"input": x}, args.steps, args.warmup,
@@ -169,7 +170,7 @@ def bench_resnet(args, cache_dir: str) -> dict:
 
     per_op = sorted(((kernel_ms[i], ops[i].node_name, selected[i].split(":", 1)[-1], op_flops(ops[i].node_name))
                      for i in range(len(ops))), reverse=True)
-    log(f"  resnet50 bs32: {ms_per_step:.3f} ms/step, {img_s:.1f} img/s; kernel time per step: conv "
+    log(f"  resnet50 bs{batch}: {ms_per_step:.3f} ms/step, {img_s:.1f} img/s; kernel time per step: conv "
         f"{conv_ms:.3f} ms, all {sum(kernel_ms):.3f} ms (profiled graph events {sum(event_ms):.3f} ms)")
     for ms, name, var, fl in per_op:
         rate = f"{fl / (ms * 1e-3) / 1e12:6.1f} TF/s" if fl and ms > 0 else " " * 11
@@ -389,6 +390,11 @@ def main() -> int:
         result.update(value=round(r["img_s"], 2), ms_per_step=round(r["ms_per_step"], 4),
                       pct_fp32_mfma_peak=round(r["pct_fp32_mfma_peak"], 2), roofline=r["roofline"])
         result["resnet50_tflops"] = round(r["tflops"], 3)
+        # The profile-max batch of the same graph, on its own tuned engine.
+        r64 = bench_resnet(args, cache_dir, batch=64)
+        result["resnet50_bs64"] = {"img_s": round(r64["img_s"], 2), "ms_per_step": round(r64["ms_per_step"], 4),
+                                   "pct_fp32_mfma_peak": round(r64["pct_fp32_mfma_peak"], 2),
+                                   "conv_tflops": r64["roofline"]["achieved"]}
     if args.workload in ("all", "ffn"):
         f = bench_ffn(args, cache_dir)
         f.pop("selected", None)
