@@ -71,21 +71,31 @@ __device__ __forceinline__ void MaxPoolBand(const float* __restrict__ x, float* 
     }
     __syncthreads();
   }
-  for (int r = wave; r < rows_out; r += kThreads / 64) {
-    const int oh = oh0 + r;
-    for (int ow = lane; ow < out_w; ow += 64) {
-      float best = neg_inf;
-      for (int kh = 0; kh < kernel_h; ++kh) {
-        const int ih = oh * stride_h - pad_h + kh * dilation_h;
-        if (static_cast<unsigned>(ih) >= static_cast<unsigned>(h)) continue;
-        const float* line = staged ? tile + (ih - ih0) * w : src + static_cast<int64_t>(ih) * w;
-        for (int kw = 0; kw < kernel_w; ++kw) {
-          const int iw = ow * stride_w - pad_w + kw * dilation_w;
-          if (static_cast<unsigned>(iw) < static_cast<unsigned>(w)) best = fmaxf(best, line[iw]);
+  // The two sources are separate instantiations: behind one pointer that may
+  // be either, the staged reads would compile to generic (FLAT) loads
+  // instead of LDS reads.
+  auto pool_rows = [&](auto input_row) {
+    for (int r = wave; r < rows_out; r += kThreads / 64) {
+      const int oh = oh0 + r;
+      for (int ow = lane; ow < out_w; ow += 64) {
+        float best = neg_inf;
+        for (int kh = 0; kh < kernel_h; ++kh) {
+          const int ih = oh * stride_h - pad_h + kh * dilation_h;
+          if (static_cast<unsigned>(ih) >= static_cast<unsigned>(h)) continue;
+          const float* line = input_row(ih);
+          for (int kw = 0; kw < kernel_w; ++kw) {
+            const int iw = ow * stride_w - pad_w + kw * dilation_w;
+            if (static_cast<unsigned>(iw) < static_cast<unsigned>(w)) best = fmaxf(best, line[iw]);
+          }
         }
+        dst[static_cast<int64_t>(oh) * out_w + ow] = best;
       }
-      dst[static_cast<int64_t>(oh) * out_w + ow] = best;
     }
+  };
+  if (staged) {
+    pool_rows([&](int ih) { return tile + (ih - ih0) * w; });
+  } else {
+    pool_rows([&](int ih) { return src + static_cast<int64_t>(ih) * w; });
   }
 }
 
