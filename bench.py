@@ -60,7 +60,7 @@ def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str):
     from cutriton_amd import engine, workloads
 
     opts = engine.CompileOptions(tuning_mode=tuning_mode, tuning_cache_dir=cache_dir,
-                                 enable_profiling=profiling, enable_hip_graph=True,
+                                 enable_profiling=profiling, enable_cuda_graph=True,
                                  tuning_warmup_iterations=3, tuning_measurement_iterations=10)
     eng = engine.build_engine(workloads.to_model(graph), opts)
     ctx = eng.create_execution_context()

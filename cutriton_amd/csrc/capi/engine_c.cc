@@ -239,13 +239,13 @@ int ct_options_set_int(ct_options* options, const char* key, int64_t value) {
   if (options == nullptr || key == nullptr) return Invalid("option arguments are null");
   CompileOptions& o = options->options;
   const std::string k = key;
-  if (k == "enable_hip_graph") o.enable_hip_graph = value != 0;
+  if (k == "enable_cuda_graph") o.enable_cuda_graph = value != 0;
   else if (k == "enable_profiling") o.enable_profiling = value != 0;
   else if (k == "enable_transformer_fusions") o.enable_transformer_fusions = value != 0;
   else if (k == "enable_residual_epilogue_fusion") o.enable_residual_epilogue_fusion = value != 0;
   else if (k == "allow_cpu_fallback") o.allow_cpu_fallback = value != 0;
   else if (k == "device_id") o.device_id = static_cast<int>(value);
-  else if (k == "hip_graph_cache_capacity") o.hip_graph_cache_capacity = static_cast<std::size_t>(value);
+  else if (k == "cuda_graph_cache_capacity") o.cuda_graph_cache_capacity = static_cast<std::size_t>(value);
   else if (k == "tuning_warmup_iterations") o.tuning_warmup_iterations = static_cast<int>(value);
   else if (k == "tuning_measurement_iterations") o.tuning_measurement_iterations = static_cast<int>(value);
   else if (k == "tuning_mode") {
@@ -417,11 +417,11 @@ int ct_context_profile_event(const ct_context* context, int index, char* name, s
 }
 
 size_t ct_context_graph_count(const ct_context* context) {
-  return context == nullptr ? 0 : context->context->cached_hip_graph_count();
+  return context == nullptr ? 0 : context->context->cached_cuda_graph_count();
 }
 
 size_t ct_context_module_count(const ct_context* context) {
-  return context == nullptr ? 0 : context->context->loaded_hip_module_count();
+  return context == nullptr ? 0 : context->context->loaded_cuda_module_count();
 }
 
 int ct_context_selected_candidate(const ct_context* context, int op_index) {

@@ -119,14 +119,14 @@ Status Compiler::Compile(const Model& model, const CompileOptions& options, Exec
         ApplyProfilePoint(&result.mutable_graph(), options.shape_profiles.front(), ProfilePoint::kOpt));
   }
   result.set_target(options.target);
-  result.set_enable_hip_graph(options.enable_hip_graph);
+  result.set_enable_cuda_graph(options.enable_cuda_graph);
   result.set_enable_profiling(options.enable_profiling);
   TuningConfig& tuning = result.mutable_tuning_config();
   tuning.mode = options.tuning_mode;
   tuning.cache_dir = options.tuning_cache_dir;
   tuning.warmup_iterations = options.tuning_warmup_iterations;
   tuning.measurement_iterations = options.tuning_measurement_iterations;
-  result.set_hip_graph_cache_capacity(options.hip_graph_cache_capacity);
+  result.set_cuda_graph_cache_capacity(options.cuda_graph_cache_capacity);
   BackendOptions& backend_options = result.mutable_backend_options();
   backend_options.device = hip_target ? Device::HIP(options.device_id) : Device::CPU();
   backend_options.kernel_artifact_dir = options.kernel_artifact_dir;

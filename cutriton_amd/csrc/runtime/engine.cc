@@ -539,12 +539,12 @@ const TensorDesc* ExecutionContext::GetResolvedTensorDesc(const std::string& nam
   return value == nullptr ? nullptr : &value->tensor;
 }
 
-std::size_t ExecutionContext::cached_hip_graph_count() const {
+std::size_t ExecutionContext::cached_cuda_graph_count() const {
   const auto* hip = static_cast<const HipExecutionState*>(hip_state_);
   return hip == nullptr ? 0 : hip->graphs.size();
 }
 
-std::size_t ExecutionContext::loaded_hip_module_count() const {
+std::size_t ExecutionContext::loaded_cuda_module_count() const {
   return state_ == nullptr ? 0 : LoadedModuleCount(state_->module_cache);
 }
 
@@ -995,7 +995,7 @@ Status ExecutionContext::RunAsync(void* stream) {
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_set_device(device.id), "hipSetDevice"));
   hip->active_stream = stream == nullptr ? hip->owned_stream : stream;
 
-  if (!state_->plan.enable_hip_graph()) {
+  if (!state_->plan.enable_cuda_graph()) {
     CUTRITON_RETURN_IF_ERROR(EnqueueOps(hip->active_stream, false));
     run_pending_ = true;
     return Status::OK();
@@ -1024,7 +1024,7 @@ Status ExecutionContext::RunAsync(void* stream) {
     created.key = graph_key;
     StageTimer timer("graph capture");
     CUTRITON_RETURN_IF_ERROR(CaptureGraph(hip->active_stream, &created.exec));
-    const std::size_t capacity = std::max<std::size_t>(1, state_->plan.hip_graph_cache_capacity());
+    const std::size_t capacity = std::max<std::size_t>(1, state_->plan.cuda_graph_cache_capacity());
     if (hip->graphs.size() >= capacity) {
       auto oldest = std::min_element(hip->graphs.begin(), hip->graphs.end(),
                                      [](const GraphEntry& a, const GraphEntry& b) { return a.last_used < b.last_used; });

@@ -223,14 +223,14 @@ class CompileOptions:
     kernel_artifact_dir: str = str(PACK_DIR)
     kernel_artifact_paths: list[str] = field(default_factory=list)
     tuning_cache_dir: str = ""
-    enable_hip_graph: bool = True
+    enable_cuda_graph: bool = True
     enable_profiling: bool = True
     enable_transformer_fusions: bool = True
     enable_residual_epilogue_fusion: bool = True
     allow_cpu_fallback: bool = False
     device_id: int = 0
     tuning_mode: str = "use_cache"
-    hip_graph_cache_capacity: int = 4
+    cuda_graph_cache_capacity: int = 4
     tuning_warmup_iterations: int = 5
     tuning_measurement_iterations: int = 20
     # name -> {input: (min, opt, max)}
@@ -246,9 +246,9 @@ class CompileOptions:
                     _check(lib.ct_options_set_string(h, _b(key), _b(value)))
             for path in self.kernel_artifact_paths:
                 _check(lib.ct_options_set_string(h, b"kernel_artifact_path", _b(path)))
-            for key in ("enable_hip_graph", "enable_profiling", "enable_transformer_fusions",
+            for key in ("enable_cuda_graph", "enable_profiling", "enable_transformer_fusions",
                         "enable_residual_epilogue_fusion", "allow_cpu_fallback", "device_id",
-                        "hip_graph_cache_capacity", "tuning_warmup_iterations", "tuning_measurement_iterations"):
+                        "cuda_graph_cache_capacity", "tuning_warmup_iterations", "tuning_measurement_iterations"):
                 _check(lib.ct_options_set_int(h, _b(key), int(getattr(self, key))))
             _check(lib.ct_options_set_int(h, b"tuning_mode", TUNING_MODES[self.tuning_mode]))
             for profile, inputs in self.shape_profiles.items():
@@ -407,10 +407,10 @@ class ExecutionContext:
             out.append((name.value.decode(), ms.value))
         return out
 
-    def cached_hip_graph_count(self) -> int:
+    def cached_cuda_graph_count(self) -> int:
         return self._lib.ct_context_graph_count(self.handle)
 
-    def loaded_hip_module_count(self) -> int:
+    def loaded_cuda_module_count(self) -> int:
         return self._lib.ct_context_module_count(self.handle)
 
     def time_op(self, op_index: int, iterations: int = 20, stream: int | None = None) -> float:

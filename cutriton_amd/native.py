@@ -89,9 +89,31 @@ def build_kernel_pack(jobs: int = 8) -> Path:
     return PACK_DIR / "pack.json"
 
 
+CPP_TEST_DIR = REPO_DIR / "tests" / "cpp"
+CPP_TEST_BIN_DIR = CPP_TEST_DIR / "bin"
+
+
+def build_cpp_gpu_test() -> Path:
+    """Compiles tests/cpp/test_hip.cc (the C++ API on the GPU) against the
+    engine library into tests/cpp/bin/test_hip. The binary finds the library
+    through a run path relative to itself, so it runs from any copy of the
+    tree."""
+    CPP_TEST_BIN_DIR.mkdir(parents=True, exist_ok=True)
+    exe = CPP_TEST_BIN_DIR / "test_hip"
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE_DIR}", f"-I{ROCM / 'include'}",
+           str(CPP_TEST_DIR / "test_hip.cc"), f"-L{PACKAGE_DIR}", "-lcutriton_gfx950", f"-L{ROCM / 'lib'}",
+           "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../../cutriton_amd", f"-Wl,-rpath,{ROCM / 'lib'}",
+           "-o", str(exe)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"g++ failed for test_hip.cc:\n{result.stderr}")
+    return exe
+
+
 def build_all(jobs: int = 8) -> None:
     build_engine_library(jobs)
     build_kernel_pack(jobs)
+    build_cpp_gpu_test()
 
 
 _LIBRARY: ctypes.CDLL | None = None

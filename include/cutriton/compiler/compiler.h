@@ -21,7 +21,7 @@ struct CompileOptions {
   std::string target{kHipBackendName};
   bool allow_cpu_fallback{false};
   // Capture the op sequence into a hipGraph on first run, replay afterwards.
-  bool enable_hip_graph{true};
+  bool enable_cuda_graph{true};
   bool enable_profiling{true};
   bool enable_transformer_fusions{true};
   // Fold a residual AddRelu into the preceding FusedConvBatchNorm epilogue.
@@ -32,7 +32,7 @@ struct CompileOptions {
   std::string tuning_cache_dir;
   TuningMode tuning_mode{TuningMode::kUseCache};
   std::vector<ShapeProfile> shape_profiles;
-  std::size_t hip_graph_cache_capacity{4};
+  std::size_t cuda_graph_cache_capacity{4};
   int tuning_warmup_iterations{5};
   int tuning_measurement_iterations{20};
 };

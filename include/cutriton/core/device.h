@@ -22,7 +22,8 @@ struct Device {
 
 struct DeviceProperties {
   Device device;
-  int compute_unit_count{0};
+  // Compute units (CUs) of the HIP device; the reference's field name.
+  int sm_count{0};
   std::size_t l2_cache_bytes{0};
   std::size_t global_memory_bytes{0};
 };

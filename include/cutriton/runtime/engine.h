@@ -50,8 +50,8 @@ class ExecutionContext {
   Status Synchronize();
 
   const Profiler& profiler() const { return profiler_; }
-  std::size_t cached_hip_graph_count() const;
-  std::size_t loaded_hip_module_count() const;
+  std::size_t cached_cuda_graph_count() const;
+  std::size_t loaded_cuda_module_count() const;
   const std::unordered_map<std::string, Tensor>& tensors() const { return tensors_; }
   // Index of the chosen candidate per plan op (valid after the first run).
   const std::vector<std::size_t>& selected_candidates() const { return selected_candidates_; }

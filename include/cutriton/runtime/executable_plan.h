@@ -48,14 +48,14 @@ class ExecutablePlan {
   // Host tensors; uploaded to the device once per Engine.
   const std::unordered_map<std::string, Tensor>& constants() const { return constants_; }
   std::unordered_map<std::string, Tensor>& mutable_constants() { return constants_; }
-  bool enable_hip_graph() const { return enable_hip_graph_; }
-  void set_enable_hip_graph(bool value) { enable_hip_graph_ = value; }
+  bool enable_cuda_graph() const { return enable_cuda_graph_; }
+  void set_enable_cuda_graph(bool value) { enable_cuda_graph_ = value; }
   bool enable_profiling() const { return enable_profiling_; }
   void set_enable_profiling(bool value) { enable_profiling_ = value; }
   const TuningConfig& tuning_config() const { return tuning_config_; }
   TuningConfig& mutable_tuning_config() { return tuning_config_; }
-  std::size_t hip_graph_cache_capacity() const { return hip_graph_cache_capacity_; }
-  void set_hip_graph_cache_capacity(std::size_t value) { hip_graph_cache_capacity_ = value; }
+  std::size_t cuda_graph_cache_capacity() const { return cuda_graph_cache_capacity_; }
+  void set_cuda_graph_cache_capacity(std::size_t value) { cuda_graph_cache_capacity_ = value; }
   const std::vector<ProfilePlan>& profile_plans() const { return profile_plans_; }
   std::vector<ProfilePlan>& mutable_profile_plans() { return profile_plans_; }
 
@@ -66,10 +66,10 @@ class ExecutablePlan {
   std::string target_;
   BackendOptions backend_options_;
   std::unordered_map<std::string, Tensor> constants_;
-  bool enable_hip_graph_{false};
+  bool enable_cuda_graph_{false};
   bool enable_profiling_{false};
   TuningConfig tuning_config_;
-  std::size_t hip_graph_cache_capacity_{4};
+  std::size_t cuda_graph_cache_capacity_{4};
   std::vector<ProfilePlan> profile_plans_;
 };
 

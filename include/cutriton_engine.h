@@ -82,10 +82,10 @@ void ct_options_destroy(ct_options* options);
 /* Keys: "target", "kernel_artifact_dir", "kernel_artifact_path" (appends),
  * "tuning_cache_dir". */
 int ct_options_set_string(ct_options* options, const char* key, const char* value);
-/* Keys: "enable_hip_graph", "enable_profiling", "enable_transformer_fusions",
+/* Keys: "enable_cuda_graph", "enable_profiling", "enable_transformer_fusions",
  * "enable_residual_epilogue_fusion", "device_id", "tuning_mode"
  * (0 disabled, 1 use-cache, 2 tune-on-miss, 3 force-retune),
- * "hip_graph_cache_capacity", "tuning_warmup_iterations",
+ * "cuda_graph_cache_capacity", "tuning_warmup_iterations",
  * "tuning_measurement_iterations", "allow_cpu_fallback". */
 int ct_options_set_int(ct_options* options, const char* key, int64_t value);
 /* Adds (or extends) shape profile `profile` with a range for `input`. */

@@ -108,7 +108,7 @@ void UseHostBackend() {
 CompileOptions HostOptions() {
   CompileOptions options;
   options.target = "mock";
-  options.enable_hip_graph = false;
+  options.enable_cuda_graph = false;
   return options;
 }
 
@@ -567,7 +567,7 @@ void CpuReferenceBackendIsUnsupported() {
   EXPECT_OK(RegisterBuiltinBackends());
   CompileOptions options;
   options.target = "cpu_reference";
-  options.enable_hip_graph = false;
+  options.enable_cuda_graph = false;
   std::unique_ptr<Engine> engine;
   const Status s = BuildEngine(ReluModel(4), options, &engine);
   EXPECT(s.code() == ErrorCode::kUnsupported);

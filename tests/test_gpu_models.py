@@ -28,7 +28,7 @@ def test_stem_known_answer():
     assert [op.op_type for op in eng.ops()] == ["FusedConvBatchNormRelu", "GlobalAveragePool", "Flatten", "Gemm"]
     events = ctx.profile_events()
     assert len(events) == 4 and events[2][1] == 0.0  # Flatten is a view and is not timed
-    assert ctx.cached_hip_graph_count() == 1
+    assert ctx.cached_cuda_graph_count() == 1
 
 
 def test_conv_bn_relu_single_node():
@@ -52,7 +52,7 @@ def test_resnet50_batch1():
     assert len(ops) == 57
     want = oracle.evaluate(g, {"input": x})["output"]
     check_logits(out["output"].astype(np.float64), want)
-    assert ctx.cached_hip_graph_count() == 1
+    assert ctx.cached_cuda_graph_count() == 1
 
 
 def test_resnet50_batch32_matches_single_images():
@@ -163,7 +163,7 @@ def test_resnet50_dynamic_batch_profile_32_and_64(tmp_path):
         for i in (0, batch - 1):
             want = oracle.evaluate(g, {"input": x64[i:i + 1]})["output"]
             check_logits(out[i:i + 1].astype(np.float64), want)
-    assert ctx.cached_hip_graph_count() == 2
+    assert ctx.cached_cuda_graph_count() == 2
 
 
 def test_ffn_dynamic_m_profile(tmp_path):
