@@ -1,9 +1,21 @@
-// Backends and lowering. Behaviour follows reference
-// src/backend/backend.cpp:22-453: the "cpu_reference" backend refuses every
-// node, the artifact backend checks device/schema/tensors, lowers a node to
-// one candidate per matching pack variant plus one FusionRegistry
-// decomposition built from default variants with named temporaries, and
-// Flatten lowers to a view. Device capability is the gfx architecture number.
+// Backends, lowering and the backend registry.
+//
+// "hip_gfx950" lowers a node in three layers:
+//   * a screen of the node itself: a HIP device, a registered schema whose
+//     arity the node meets, FP32/FP16 tensors placed on that device, and at
+//     least one pack entry for its op type (Flatten needs none: it is a view
+//     and refused only as a graph output, which would need a copy);
+//   * KernelFit, which decides whether one pack entry can run the node: the
+//     device's architecture, the entry's dtype and layout, constant re-layouts
+//     (OHWI / NK / T copies of constant inputs), and the declarative
+//     constraints of the entry;
+//   * candidates: one per fitting entry, then one per FusionRegistry
+//     alternative whose recipe (the unfused op sequence) finds a fitting
+//     default entry for every step; recipe intermediates are candidate
+//     temporaries shaped like the fused output.
+// The reference's lowering (src/backend/backend.cpp) yields the same
+// candidate set: fused entries first, the decomposition last, defaults as the
+// pack flags them; "cpu_reference" refuses every node.
 #include "cutriton/backend/backend.h"
 
 #include <algorithm>
@@ -20,6 +32,8 @@
 namespace cutriton {
 namespace {
 
+using ValueLookup = std::function<const ValueDesc*(const std::string&)>;
+
 class CpuReferenceBackend final : public Backend {
  public:
   const char* name() const override { return "cpu_reference"; }
@@ -32,160 +46,276 @@ class CpuReferenceBackend final : public Backend {
   }
 };
 
-// Flatten shares its input's memory; nothing is launched.
+// Flatten: the output shares the input's memory; nothing is launched.
 class ViewKernel final : public OpKernel {
  public:
   const char* backend_name() const override { return kHipBackendName; }
   const char* op_type() const override { return "Flatten"; }
   Status Compute(KernelContext* context) override {
-    if (context == nullptr || context->node == nullptr || context->tensors == nullptr) {
-      return Status::InvalidArgument("Flatten KernelContext is invalid");
-    }
-    return Status::OK();
+    const bool valid = context != nullptr && context->node != nullptr && context->tensors != nullptr;
+    return valid ? Status::OK() : Status::InvalidArgument("Flatten KernelContext is invalid");
   }
 };
 
-using ValueLookup = std::function<const ValueDesc*(const std::string&)>;
-
-Status CheckTensor(const Graph& graph, const std::string& name, const Device& device) {
-  const ValueDesc* value = graph.FindValue(name);
-  if (value == nullptr) return Status::NotFound("tensor description is missing: " + name);
-  CUTRITON_RETURN_IF_ERROR(value->tensor.Validate());
-  if (value->tensor.dtype != DataType::kFloat32 && value->tensor.dtype != DataType::kFloat16) {
-    return Status::Unsupported("only float32/float16 tensors are supported: " + name);
-  }
-  if (value->tensor.device_type != device.type || value->tensor.device_id != device.id) {
-    return Status::Unsupported("tensor is assigned to another device: " + name);
-  }
-  return Status::OK();
+const std::string& ValueName(const Node& node, bool output, int index) {
+  static const std::string kNone;
+  const auto& names = output ? node.outputs() : node.inputs();
+  return index >= 0 && static_cast<std::size_t>(index) < names.size() ? names[static_cast<std::size_t>(index)] : kNone;
 }
 
-std::vector<std::string> InvocationInputs(const KernelArtifact& artifact, std::vector<std::string> inputs) {
-  for (const auto& argument : artifact.arguments) {
-    const KernelArgumentSource& s = argument.source;
-    if (s.layout.empty() || s.index < 0 || static_cast<std::size_t>(s.index) >= inputs.size()) continue;
-    std::string& name = inputs[static_cast<std::size_t>(s.index)];
-    name = LaidOutConstantName(name, s.layout);
+// Whether a pack entry can run a node on a device of numeric architecture
+// `capability` (named `arch`).
+class KernelFit {
+ public:
+  KernelFit(int capability, std::string arch) : capability_(capability), arch_(std::move(arch)) {}
+
+  bool Accepts(const KernelArtifact& entry, const Node& node, const ValueLookup& lookup) const {
+    return RunsOnDevice(entry) && TypesMatch(entry, node, lookup) && ConstantLayoutsMatch(entry, node, lookup) &&
+           std::all_of(entry.constraints.begin(), entry.constraints.end(),
+                       [&](const KernelConstraint& c) { return Holds(c, node, lookup); });
+  }
+
+ private:
+  bool RunsOnDevice(const KernelArtifact& entry) const {
+    return entry.min_compute_capability <= capability_ && (entry.target_arch.empty() || entry.target_arch == arch_);
+  }
+
+  // The entry's dtype is the node's (its first output, else first input);
+  // its layout, when set, that of the first input and of every output.
+  static bool TypesMatch(const KernelArtifact& entry, const Node& node, const ValueLookup& lookup) {
+    const ValueDesc* typed = lookup(node.outputs().empty() ? node.inputs().front() : node.outputs().front());
+    if (typed == nullptr || entry.dtype != DataTypeName(typed->tensor.dtype)) return false;
+    auto in_layout = [&](const std::string& name) {
+      const ValueDesc* value = lookup(name);
+      return value != nullptr && (entry.layout.empty() || value->tensor.layout == entry.layout);
+    };
+    if (!node.inputs().empty() && !in_layout(node.inputs().front())) return false;
+    return std::all_of(node.outputs().begin(), node.outputs().end(), in_layout);
+  }
+
+  // An argument read in another layout must be a constant of a shape that
+  // layout is defined for (the engine makes the copy at constant upload).
+  static bool ConstantLayoutsMatch(const KernelArtifact& entry, const Node& node, const ValueLookup& lookup) {
+    for (const auto& argument : entry.arguments) {
+      const std::string& layout = argument.source.layout;
+      if (layout.empty()) continue;
+      const ValueDesc* value = lookup(ValueName(node, false, argument.source.index));
+      if (value == nullptr || !value->is_constant) return false;
+      const std::size_t rank = value->tensor.shape.size();
+      const bool defined = layout == "OHWI" ? rank == 4 && value->tensor.dtype == DataType::kFloat32
+                                            : (layout == "NK" || layout == "T") && rank == 2;
+      if (!defined) return false;
+    }
+    return true;
+  }
+
+  static bool Holds(const KernelConstraint& c, const Node& node, const ValueLookup& lookup) {
+    switch (c.kind) {
+      case KernelConstraintKind::kInputCountEquals:
+        return node.inputs().size() == static_cast<std::size_t>(c.expected);
+      case KernelConstraintKind::kAttributeInt64Equals:
+        return GetIntAttribute(node, c.attribute_name, c.default_value) == c.expected;
+      case KernelConstraintKind::kTensorRankEquals:
+      case KernelConstraintKind::kTensorDimAtMost: {
+        const ValueDesc* value = lookup(ValueName(node, c.tensor_is_output, c.tensor_index));
+        if (value == nullptr) return false;
+        const auto& shape = value->tensor.shape;
+        if (c.kind == KernelConstraintKind::kTensorRankEquals) return shape.size() == static_cast<std::size_t>(c.expected);
+        return static_cast<std::size_t>(c.tensor_axis) < shape.size() && shape[static_cast<std::size_t>(c.tensor_axis)] <= c.expected;
+      }
+      case KernelConstraintKind::kTensorBytesAtMost:
+        for (const auto* names : {&node.inputs(), &node.outputs()}) {
+          for (const auto& name : *names) {
+            const ValueDesc* value = lookup(name);
+            if (value == nullptr || static_cast<int64_t>(value->tensor.ByteSize()) > c.expected) return false;
+          }
+        }
+        return true;
+    }
+    return false;
+  }
+
+  int capability_;
+  std::string arch_;
+};
+
+// Inputs of a kernel step: constants read in another layout are bound under
+// the name of their re-laid-out copy.
+std::vector<std::string> StepInputs(const KernelArtifact& entry, std::vector<std::string> inputs) {
+  for (const auto& argument : entry.arguments) {
+    const int index = argument.source.index;
+    if (argument.source.layout.empty() || index < 0 || static_cast<std::size_t>(index) >= inputs.size()) continue;
+    inputs[static_cast<std::size_t>(index)] = LaidOutConstantName(inputs[static_cast<std::size_t>(index)], argument.source.layout);
   }
   return inputs;
 }
 
-std::string BaseArch(const std::string& full) {
-  const auto colon = full.find(':');
-  return colon == std::string::npos ? full : full.substr(0, colon);
+// The unfused op sequence of a fused op. Operands name the fused node's
+// inputs ("in0".."in6", "in*" for all of them), its output ("out") or a
+// temporary ("t0", "t1": workspace slots 0 and 1, shaped like the output).
+struct RecipeStep {
+  const char* op;
+  std::vector<const char*> inputs;
+  const char* output;
+};
+
+const std::map<std::string, std::vector<RecipeStep>>& Recipes() {
+  static const std::map<std::string, std::vector<RecipeStep>> recipes = {
+      {"FusedConvBatchNormRelu",
+       {{"Conv", {"in0", "in1"}, "t0"},
+        {"BatchNormalization", {"t0", "in2", "in3", "in4", "in5"}, "t1"},
+        {"Relu", {"t1"}, "out"}}},
+      {"FusedConvBatchNorm",
+       {{"Conv", {"in0", "in1"}, "t0"}, {"BatchNormalization", {"t0", "in2", "in3", "in4", "in5"}, "out"}}},
+      {"FusedConvBatchNormAddRelu",
+       {{"FusedConvBatchNorm", {"in0", "in1", "in2", "in3", "in4", "in5"}, "t0"}, {"AddRelu", {"t0", "in6"}, "out"}}},
+      {"AddRelu", {{"Add", {"in0", "in1"}, "t0"}, {"Relu", {"t0"}, "out"}}},
+      {"GemmGelu", {{"Gemm", {"in*"}, "t0"}, {"Gelu", {"t0"}, "out"}}},
+      {"SkipLayerNormalization",
+       {{"Add", {"in0", "in1"}, "t0"}, {"LayerNormalization", {"t0", "in2", "in3"}, "out"}}},
+  };
+  return recipes;
 }
 
-bool ArtifactMatches(const KernelArtifact& artifact, const Node& node, const ValueLookup& lookup,
-                     int capability, const std::string& arch) {
-  if (capability < artifact.min_compute_capability) return false;
-  if (!artifact.target_arch.empty() && artifact.target_arch != arch) return false;
-  const std::string& reference_name =
-      node.outputs().empty() ? node.inputs().front() : node.outputs().front();
-  const ValueDesc* reference = lookup(reference_name);
-  if (reference == nullptr || artifact.dtype != DataTypeName(reference->tensor.dtype)) return false;
-  auto layout_ok = [&](const std::string& name) {
-    const ValueDesc* v = lookup(name);
-    return v != nullptr && (artifact.layout.empty() || v->tensor.layout == artifact.layout);
-  };
-  if (!node.inputs().empty() && !layout_ok(node.inputs().front())) return false;
-  for (const auto& name : node.outputs()) {
-    if (!layout_ok(name)) return false;
-  }
-  // An input read in another layout must be a constant (the engine re-lays
-  // it out once, at constant upload): rank-4 FP32 for OHWI, rank 2 for NK and T.
-  for (const auto& argument : artifact.arguments) {
-    const KernelArgumentSource& s = argument.source;
-    if (s.layout.empty()) continue;
-    if (s.index < 0 || static_cast<std::size_t>(s.index) >= node.inputs().size()) return false;
-    const ValueDesc* v = lookup(node.inputs()[static_cast<std::size_t>(s.index)]);
-    if (v == nullptr || !v->is_constant) return false;
-    const bool ohwi = s.layout == "OHWI" && v->tensor.shape.size() == 4 && v->tensor.dtype == DataType::kFloat32;
-    const bool nk = (s.layout == "NK" || s.layout == "T") && v->tensor.shape.size() == 2;
-    if (!ohwi && !nk) return false;
-  }
-  for (const auto& c : artifact.constraints) {
-    switch (c.kind) {
-      case KernelConstraintKind::kInputCountEquals:
-        if (node.inputs().size() != static_cast<std::size_t>(c.expected)) return false;
-        break;
-      case KernelConstraintKind::kAttributeInt64Equals:
-        if (GetIntAttribute(node, c.attribute_name, c.default_value) != c.expected) return false;
-        break;
-      case KernelConstraintKind::kTensorRankEquals: {
-        const auto& names = c.tensor_is_output ? node.outputs() : node.inputs();
-        if (c.tensor_index < 0 || static_cast<std::size_t>(c.tensor_index) >= names.size()) {
-          return false;
-        }
-        const ValueDesc* v = lookup(names[static_cast<std::size_t>(c.tensor_index)]);
-        if (v == nullptr || v->tensor.shape.size() != static_cast<std::size_t>(c.expected)) {
-          return false;
-        }
-        break;
-      }
-      case KernelConstraintKind::kTensorDimAtMost: {
-        const auto& names = c.tensor_is_output ? node.outputs() : node.inputs();
-        if (c.tensor_index < 0 || static_cast<std::size_t>(c.tensor_index) >= names.size()) {
-          return false;
-        }
-        const ValueDesc* v = lookup(names[static_cast<std::size_t>(c.tensor_index)]);
-        if (v == nullptr || static_cast<std::size_t>(c.tensor_axis) >= v->tensor.shape.size() ||
-            v->tensor.shape[static_cast<std::size_t>(c.tensor_axis)] > c.expected) {
-          return false;
-        }
-        break;
-      }
+class HipLowering {
+ public:
+  HipLowering(const Node& node, const Graph& graph, const ArtifactRepository& repository, KernelFit fit)
+      : node_(node), graph_(graph), repository_(repository), fit_(std::move(fit)) {}
+
+  // One candidate per pack entry that fits the node.
+  void AddFusedEntries(const KernelCatalog& catalog, int capability, std::vector<ExecutionCandidate>* out) const {
+    const ValueLookup lookup = [&](const std::string& name) { return graph_.FindValue(name); };
+    const std::string dtype = DataTypeName(graph_.FindValue(node_.outputs().front())->tensor.dtype);
+    const std::string layout = node_.inputs().empty() ? std::string() : graph_.FindValue(node_.inputs().front())->tensor.layout;
+    for (const KernelArtifact* entry : catalog.Query(node_.op_type(), dtype, layout, capability)) {
+      if (!fit_.Accepts(*entry, node_, lookup)) continue;
+      ExecutionCandidate candidate;
+      candidate.candidate_id = entry->identity();
+      candidate.is_default = entry->is_default;
+      candidate.steps.push_back(KernelInvocation{*entry, StepInputs(*entry, node_.inputs()), node_.outputs()});
+      out->push_back(std::move(candidate));
     }
   }
-  return true;
-}
 
-Status CheckHipNode(const Node& node, const Graph& graph, const BackendOptions& options,
-                    const ArtifactRepository& repository) {
+  // The decomposition of `alternative`, or false when a step has no default
+  // entry that fits it.
+  bool BuildDecomposition(const FusionAlternative& alternative, ExecutionCandidate* candidate) const {
+    const auto recipe = Recipes().find(node_.op_type());
+    if (recipe == Recipes().end()) return false;
+    const std::string& output = node_.outputs().front();
+    const std::string dtype = DataTypeName(graph_.FindValue(output)->tensor.dtype);
+    std::map<std::string, std::string> temporaries;  // operand -> value name
+    auto resolve = [&](const std::string& operand, std::vector<std::string>* names) {
+      if (operand == "out") {
+        names->push_back(output);
+      } else if (operand == "in*") {
+        names->insert(names->end(), node_.inputs().begin(), node_.inputs().end());
+      } else if (operand.rfind("in", 0) == 0) {
+        names->push_back(node_.inputs().at(static_cast<std::size_t>(std::stoi(operand.substr(2)))));
+      } else {
+        auto [slot, fresh] = temporaries.try_emplace(operand, node_.name() + "::" + operand);
+        if (fresh) {
+          candidate->temporaries.push_back(
+              CandidateTemporary{slot->second, output, static_cast<std::size_t>(std::stoi(operand.substr(1)))});
+        }
+        names->push_back(slot->second);
+      }
+    };
+    // Temporaries are described like the fused output.
+    const ValueLookup lookup = [&](const std::string& name) -> const ValueDesc* {
+      for (const auto& temporary : candidate->temporaries) {
+        if (temporary.name == name) return graph_.FindValue(output);
+      }
+      return graph_.FindValue(name);
+    };
+    candidate->candidate_id = alternative.candidate_id;
+    for (const RecipeStep& step : recipe->second) {
+      std::vector<std::string> inputs;
+      std::vector<std::string> outputs;
+      for (const char* operand : step.inputs) resolve(operand, &inputs);
+      resolve(step.output, &outputs);
+      // The step is a node of its own carrying the fused node's attributes.
+      Node probe(node_.name(), step.op, inputs, outputs);
+      for (const auto& [key, value] : node_.attributes()) probe.SetAttribute(key, value);
+      const auto* entries = repository_.Find(step.op);
+      const KernelArtifact* chosen = nullptr;
+      for (std::size_t i = 0; entries != nullptr && i < entries->size() && chosen == nullptr; ++i) {
+        const KernelArtifact& entry = (*entries)[i];
+        if (entry.is_default && entry.dtype == dtype && fit_.Accepts(entry, probe, lookup)) chosen = &entry;
+      }
+      if (chosen == nullptr) return false;
+      candidate->steps.push_back(KernelInvocation{*chosen, StepInputs(*chosen, inputs), outputs});
+    }
+    return true;
+  }
+
+ private:
+  const Node& node_;
+  const Graph& graph_;
+  const ArtifactRepository& repository_;
+  KernelFit fit_;
+};
+
+std::string BaseArch(const std::string& full) { return full.substr(0, full.find(':')); }
+
+// What every HIP node must satisfy before its pack entries are consulted.
+Status ScreenHipNode(const Node& node, const Graph& graph, const BackendOptions& options,
+                     const ArtifactRepository& repository) {
   if (options.device.type != DeviceType::kHIP) {
     return Status::Unsupported(std::string(kHipBackendName) + " requires a HIP device");
   }
   CUTRITON_RETURN_IF_ERROR(RegisterBuiltinOpSchemas());
   const auto schema = OpSchemaRegistry::Global().Find(node.op_type());
   if (schema == nullptr) return Status::Unsupported("no OpSchema is registered for " + node.op_type());
-  if (node.inputs().size() < schema->min_inputs || node.inputs().size() > schema->max_inputs ||
-      node.outputs().size() != schema->outputs) {
+  const std::size_t inputs = node.inputs().size();
+  if (inputs < schema->min_inputs || inputs > schema->max_inputs || node.outputs().size() != schema->outputs) {
     return Status::Unsupported(node.op_type() + " has an invalid input/output count");
   }
-  for (const auto& name : node.inputs()) CUTRITON_RETURN_IF_ERROR(CheckTensor(graph, name, options.device));
-  for (const auto& name : node.outputs()) CUTRITON_RETURN_IF_ERROR(CheckTensor(graph, name, options.device));
+  for (const auto* names : {&node.inputs(), &node.outputs()}) {
+    for (const auto& name : *names) {
+      const ValueDesc* value = graph.FindValue(name);
+      if (value == nullptr) return Status::NotFound("tensor description is missing: " + name);
+      CUTRITON_RETURN_IF_ERROR(value->tensor.Validate());
+      const DataType dtype = value->tensor.dtype;
+      if (dtype != DataType::kFloat32 && dtype != DataType::kFloat16) {
+        return Status::Unsupported("only float32/float16 tensors are supported: " + name);
+      }
+      if (value->tensor.device_type != options.device.type || value->tensor.device_id != options.device.id) {
+        return Status::Unsupported("tensor is assigned to another device: " + name);
+      }
+    }
+  }
   if (node.op_type() == "Flatten") {
-    const auto& outs = graph.outputs();
-    if (std::find(outs.begin(), outs.end(), node.outputs().front()) != outs.end()) {
+    const auto& outputs = graph.outputs();
+    if (std::find(outputs.begin(), outputs.end(), node.outputs().front()) != outputs.end()) {
       return Status::Unsupported("a Flatten graph output needs an explicit copy kernel");
     }
     return Status::OK();
   }
-  const auto* artifacts = repository.Find(node.op_type());
-  if (artifacts == nullptr || artifacts->empty()) {
-    return Status::Unsupported("no Kernel Pack entry for " + node.op_type());
-  }
+  const auto* entries = repository.Find(node.op_type());
+  if (entries == nullptr || entries->empty()) return Status::Unsupported("no Kernel Pack entry for " + node.op_type());
   int capability = 0;
   std::string arch;
   CUTRITON_RETURN_IF_ERROR(DeviceArchitecture(options.device.id, &capability, &arch));
-  const ValueLookup lookup = [&](const std::string& n) { return graph.FindValue(n); };
-  for (const auto& artifact : *artifacts) {
-    if (ArtifactMatches(artifact, node, lookup, capability, arch)) return Status::OK();
-  }
-  return Status::Unsupported("no Kernel Pack variant of " + node.op_type() +
-                             " matches dtype/layout/architecture/constraints");
+  const KernelFit fit(capability, arch);
+  const ValueLookup lookup = [&](const std::string& name) { return graph.FindValue(name); };
+  const bool any = std::any_of(entries->begin(), entries->end(),
+                               [&](const KernelArtifact& entry) { return fit.Accepts(entry, node, lookup); });
+  return any ? Status::OK()
+             : Status::Unsupported("no Kernel Pack variant of " + node.op_type() +
+                                   " matches dtype/layout/architecture/constraints");
 }
 
 class HipBackend final : public Backend {
  public:
   const char* name() const override { return kHipBackendName; }
 
-  Status CheckSupport(const Node& node, const Graph& graph,
-                      const BackendOptions& options) const override {
+  Status CheckSupport(const Node& node, const Graph& graph, const BackendOptions& options) const override {
     std::vector<std::string> paths = options.kernel_artifact_paths;
     if (paths.empty() && !options.kernel_artifact_dir.empty()) paths.push_back(options.kernel_artifact_dir);
     ArtifactRepository repository;
     CUTRITON_RETURN_IF_ERROR(repository.Load(paths));
-    return CheckHipNode(node, graph, options, repository);
+    return ScreenHipNode(node, graph, options, repository);
   }
 
   Status Lower(const Node& node, const LoweringContext& context,
@@ -194,8 +324,7 @@ class HipBackend final : public Backend {
         context.artifacts == nullptr || context.catalog == nullptr) {
       return Status::InvalidArgument("HIP lowering context is incomplete");
     }
-    const Graph& graph = *context.graph;
-    CUTRITON_RETURN_IF_ERROR(CheckHipNode(node, graph, *context.options, *context.artifacts));
+    CUTRITON_RETURN_IF_ERROR(ScreenHipNode(node, *context.graph, *context.options, *context.artifacts));
     candidates->clear();
     if (node.op_type() == "Flatten") {
       ExecutionCandidate view;
@@ -208,110 +337,29 @@ class HipBackend final : public Backend {
     int capability = 0;
     std::string arch;
     CUTRITON_RETURN_IF_ERROR(DeviceArchitecture(context.options->device.id, &capability, &arch));
-    const ValueDesc* out = graph.FindValue(node.outputs().front());
-    if (out == nullptr) return Status::NotFound("lowered node output description is missing");
-    const std::string dtype = DataTypeName(out->tensor.dtype);
-    const std::string layout =
-        node.inputs().empty() ? std::string() : graph.FindValue(node.inputs().front())->tensor.layout;
-    const ValueLookup graph_lookup = [&](const std::string& n) { return graph.FindValue(n); };
-    for (const KernelArtifact* artifact : context.catalog->Query(node.op_type(), dtype, layout, capability)) {
-      if (!ArtifactMatches(*artifact, node, graph_lookup, capability, arch)) continue;
-      ExecutionCandidate candidate;
-      candidate.candidate_id = artifact->identity();
-      candidate.is_default = artifact->is_default;
-      candidate.steps.push_back(
-          KernelInvocation{*artifact, InvocationInputs(*artifact, node.inputs()), node.outputs()});
-      candidates->push_back(std::move(candidate));
-    }
+    const HipLowering lowering(node, *context.graph, *context.artifacts, KernelFit(capability, arch));
+    lowering.AddFusedEntries(*context.catalog, capability, candidates);
     CUTRITON_RETURN_IF_ERROR(RegisterBuiltinFusionAlternatives());
     for (const auto& alternative : FusionRegistry::Global().Find(node.op_type())) {
       ExecutionCandidate candidate;
-      candidate.candidate_id = alternative.candidate_id;
-      if (Decompose(node, graph, *context.artifacts, dtype, capability, arch, &candidate)) {
-        candidates->push_back(std::move(candidate));
-      }
+      if (lowering.BuildDecomposition(alternative, &candidate)) candidates->push_back(std::move(candidate));
     }
-    return candidates->empty() ? Status::Unsupported("no compatible artifact for " + node.op_type())
-                               : Status::OK();
+    if (candidates->empty()) return Status::Unsupported("no compatible artifact for " + node.op_type());
+    return Status::OK();
   }
 
   Status CreateKernel(const Node& node, const Graph&, const BackendOptions&,
                       std::unique_ptr<OpKernel>* kernel) const override {
     if (kernel == nullptr) return Status::InvalidArgument("OpKernel output pointer is null");
-    if (node.op_type() == "Flatten") {
-      *kernel = std::make_unique<ViewKernel>();
-      return Status::OK();
+    if (node.op_type() != "Flatten") {
+      return Status::Unsupported("artifact kernels are instantiated from KernelInvocations");
     }
-    return Status::Unsupported("artifact kernels are instantiated from KernelInvocations");
-  }
-
- private:
-  // Builds the unfused step sequence of `node`. Each step uses the default
-  // variant of its op whose constraints accept the step; temporaries take
-  // the fused output's description and numbered workspace slots.
-  static bool Decompose(const Node& node, const Graph& graph, const ArtifactRepository& repository,
-                        const std::string& dtype, int capability, const std::string& arch,
-                        ExecutionCandidate* candidate) {
-    const std::string& out = node.outputs().front();
-    std::map<std::string, std::string> temporaries;  // name -> like value
-    const ValueLookup lookup = [&](const std::string& n) -> const ValueDesc* {
-      const auto t = temporaries.find(n);
-      return graph.FindValue(t == temporaries.end() ? n : t->second);
-    };
-    auto step = [&](const char* op, std::vector<std::string> inputs, std::string output) -> bool {
-      Node probe(node.name(), op, inputs, {output});
-      for (const auto& attribute : node.attributes()) probe.SetAttribute(attribute.first, attribute.second);
-      const auto* list = repository.Find(op);
-      if (list == nullptr) return false;
-      for (const auto& artifact : *list) {
-        if (artifact.is_default && artifact.dtype == dtype &&
-            ArtifactMatches(artifact, probe, lookup, capability, arch)) {
-          candidate->steps.push_back(
-              KernelInvocation{artifact, InvocationInputs(artifact, std::move(inputs)), {std::move(output)}});
-          return true;
-        }
-      }
-      return false;
-    };
-    auto temporary = [&](const std::string& suffix, std::size_t slot) {
-      const std::string name = node.name() + "::__" + suffix;
-      temporaries[name] = out;
-      candidate->temporaries.push_back(CandidateTemporary{name, out, slot});
-      return name;
-    };
-    const auto& in = node.inputs();
-    const std::string& op = node.op_type();
-    bool ok = false;
-    if (op == "FusedConvBatchNormRelu" || op == "FusedConvBatchNorm") {
-      const bool relu = op == "FusedConvBatchNormRelu";
-      const std::string conv = temporary("conv", 0);
-      const std::string bn = relu ? temporary("bn", 1) : out;
-      ok = step("Conv", {in[0], in[1]}, conv) &&
-           step("BatchNormalization", {conv, in[2], in[3], in[4], in[5]}, bn) &&
-           (!relu || step("Relu", {bn}, out));
-    } else if (op == "FusedConvBatchNormAddRelu") {
-      const std::string conv_bn = temporary("conv_bn", 0);
-      ok = step("FusedConvBatchNorm", {in[0], in[1], in[2], in[3], in[4], in[5]}, conv_bn) &&
-           step("AddRelu", {conv_bn, in[6]}, out);
-    } else if (op == "AddRelu") {
-      const std::string sum = temporary("add", 0);
-      ok = step("Add", in, sum) && step("Relu", {sum}, out);
-    } else if (op == "GemmGelu") {
-      const std::string projected = temporary("gemm", 0);
-      ok = step("Gemm", in, projected) && step("Gelu", {projected}, out);
-    } else if (op == "SkipLayerNormalization") {
-      const std::string sum = temporary("add", 0);
-      ok = step("Add", {in[0], in[1]}, sum) && step("LayerNormalization", {sum, in[2], in[3]}, out);
-    }
-    if (!ok) {
-      candidate->steps.clear();
-      candidate->temporaries.clear();
-    }
-    return ok;
+    *kernel = std::make_unique<ViewKernel>();
+    return Status::OK();
   }
 };
 
-Status RegisterBuiltin(std::shared_ptr<Backend> backend) {
+Status RegisterOnce(std::shared_ptr<Backend> backend) {
   auto& registry = KernelRegistry::Global();
   if (registry.GetBackend(backend->name()) != nullptr) return Status::OK();
   const Status status = registry.RegisterBackend(std::move(backend));
@@ -319,6 +367,37 @@ Status RegisterBuiltin(std::shared_ptr<Backend> backend) {
 }
 
 }  // namespace
+
+Status CheckCandidateShapes(const ExecutionCandidate& candidate, const Graph& graph) {
+  // Temporaries take the shape of their "like" value; re-laid-out constant
+  // copies keep their original's byte size.
+  auto describe = [&](std::string name) -> const ValueDesc* {
+    for (const auto& temporary : candidate.temporaries) {
+      if (temporary.name == name) name = temporary.like_value;
+    }
+    const auto copy = name.rfind('#');
+    return graph.FindValue(copy == std::string::npos ? name : name.substr(0, copy));
+  };
+  for (const auto& step : candidate.steps) {
+    const auto* invocation = std::get_if<KernelInvocation>(&step);
+    if (invocation == nullptr) continue;
+    for (const auto& constraint : invocation->artifact.constraints) {
+      if (constraint.kind != KernelConstraintKind::kTensorBytesAtMost) continue;
+      for (const auto* names : {&invocation->inputs, &invocation->outputs}) {
+        for (const auto& name : *names) {
+          const ValueDesc* value = describe(name);
+          if (value == nullptr) return Status::NotFound("tensor description is missing: " + name);
+          if (static_cast<int64_t>(value->tensor.ByteSize()) > constraint.expected) {
+            return Status::Unsupported(invocation->artifact.kernel_id + " addresses at most " +
+                                       std::to_string(constraint.expected) + " bytes per tensor; " + name + " holds " +
+                                       std::to_string(value->tensor.ByteSize()));
+          }
+        }
+      }
+    }
+  }
+  return Status::OK();
+}
 
 Status Backend::Lower(const Node& node, const LoweringContext& context,
                       std::vector<ExecutionCandidate>* candidates) const {
@@ -340,10 +419,10 @@ KernelRegistry& KernelRegistry::Global() {
 
 Status KernelRegistry::RegisterBackend(std::shared_ptr<Backend> backend) {
   if (backend == nullptr) return Status::InvalidArgument("Backend must not be null");
-  const std::string key = backend->name();
+  std::string key = backend->name();
   if (key.empty()) return Status::InvalidArgument("Backend name must not be empty");
   std::unique_lock<std::shared_mutex> lock(mutex_);
-  if (!backends_.emplace(key, std::move(backend)).second) {
+  if (!backends_.try_emplace(key, std::move(backend)).second) {
     return Status::AlreadyExists("Backend is already registered: " + key);
   }
   return Status::OK();
@@ -351,14 +430,16 @@ Status KernelRegistry::RegisterBackend(std::shared_ptr<Backend> backend) {
 
 std::shared_ptr<Backend> KernelRegistry::GetBackend(const std::string& name) const {
   std::shared_lock<std::shared_mutex> lock(mutex_);
-  const auto it = backends_.find(name);
-  return it == backends_.end() ? nullptr : it->second;
+  const auto found = backends_.find(name);
+  return found == backends_.end() ? nullptr : found->second;
 }
 
 std::vector<std::string> KernelRegistry::AvailableBackends() const {
-  std::shared_lock<std::shared_mutex> lock(mutex_);
   std::vector<std::string> names;
-  for (const auto& entry : backends_) names.push_back(entry.first);
+  {
+    std::shared_lock<std::shared_mutex> lock(mutex_);
+    for (const auto& entry : backends_) names.push_back(entry.first);
+  }
   std::sort(names.begin(), names.end());
   return names;
 }
@@ -372,37 +453,32 @@ std::shared_ptr<Backend> CreateCpuReferenceBackend() { return std::make_shared<C
 std::shared_ptr<Backend> CreateHipBackend() { return std::make_shared<HipBackend>(); }
 
 Status RegisterBuiltinBackends() {
-  CUTRITON_RETURN_IF_ERROR(RegisterBuiltin(CreateCpuReferenceBackend()));
-  CUTRITON_RETURN_IF_ERROR(RegisterBuiltin(CreateHipBackend()));
-  return Status::OK();
+  CUTRITON_RETURN_IF_ERROR(RegisterOnce(CreateCpuReferenceBackend()));
+  return RegisterOnce(CreateHipBackend());
 }
 
 Status DeviceArchitecture(int device_id, int* numeric_arch, std::string* arch_name) {
-  if (numeric_arch == nullptr || arch_name == nullptr) {
-    return Status::InvalidArgument("architecture outputs are null");
-  }
+  if (numeric_arch == nullptr || arch_name == nullptr) return Status::InvalidArgument("architecture outputs are null");
   // CUTRITON_TARGET_ARCH (e.g. "gfx950") plans for a device that is not
   // attached: lowering and memory planning then run without a GPU.
-  if (const char* forced = std::getenv("CUTRITON_TARGET_ARCH")) {
-    if (std::strncmp(forced, "gfx", 3) == 0) {
-      *arch_name = BaseArch(forced);
-      *numeric_arch = std::atoi(forced + 3);
-      return Status::OK();
-    }
+  if (const char* forced = std::getenv("CUTRITON_TARGET_ARCH"); forced != nullptr && std::strncmp(forced, "gfx", 3) == 0) {
+    *arch_name = BaseArch(forced);
+    *numeric_arch = std::atoi(forced + 3);
+    return Status::OK();
   }
   static std::mutex mutex;
-  static std::map<int, std::pair<int, std::string>> cache;
+  static std::map<int, std::pair<int, std::string>> known;
   std::lock_guard<std::mutex> lock(mutex);
-  auto it = cache.find(device_id);
-  if (it == cache.end()) {
+  auto found = known.find(device_id);
+  if (found == known.end()) {
     cth_device_info info;
     if (cth_device_query(device_id, &info) != 0) {
       return Status::RuntimeError(std::string("HIP device query failed: ") + cth_last_error());
     }
-    it = cache.emplace(device_id, std::make_pair(info.numeric_arch, BaseArch(info.arch_name))).first;
+    found = known.emplace(device_id, std::make_pair(info.numeric_arch, BaseArch(info.arch_name))).first;
   }
-  *numeric_arch = it->second.first;
-  *arch_name = it->second.second;
+  *numeric_arch = found->second.first;
+  *arch_name = found->second.second;
   return Status::OK();
 }
 

@@ -73,6 +73,11 @@ class HipModuleCache {
     return modules_.size();
   }
 
+  bool HasCodeObject(const std::string& sha256) const {
+    std::lock_guard<std::mutex> lock(mutex_);
+    return modules_.count(sha256) != 0;
+  }
+
  private:
   int device_id_;
   mutable std::mutex mutex_;
@@ -330,6 +335,10 @@ Status CreateInvocationKernel(const KernelInvocation& invocation, int device_id,
 
 std::size_t LoadedModuleCount(const std::shared_ptr<HipModuleCache>& cache) {
   return cache == nullptr ? 0 : cache->size();
+}
+
+bool CodeObjectLoaded(const std::shared_ptr<HipModuleCache>& cache, const KernelArtifact& artifact) {
+  return cache != nullptr && cache->HasCodeObject(artifact.sha256);
 }
 
 }  // namespace cutriton

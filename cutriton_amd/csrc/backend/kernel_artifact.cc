@@ -158,6 +158,9 @@ KernelConstraint ParseConstraint(const Value& v) {
     c.default_value = IntOr(v, "default", 0);
   } else if (kind == "input_count_eq") {
     c.kind = KernelConstraintKind::kInputCountEquals;
+  } else if (kind == "tensor_bytes_le") {
+    c.kind = KernelConstraintKind::kTensorBytesAtMost;
+    if (c.expected <= 0) throw std::runtime_error("tensor_bytes_le value must be positive");
   } else if (kind == "tensor_rank_eq" || kind == "dim_le") {
     c.kind = kind == "dim_le" ? KernelConstraintKind::kTensorDimAtMost : KernelConstraintKind::kTensorRankEquals;
     const std::string source = v.at("source").string();

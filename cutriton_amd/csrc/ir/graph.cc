@@ -1,11 +1,18 @@
-// Graph/Model implementation. Behaviour follows reference
-// src/ir/graph.cpp:11-229 (value registry, Kahn topological sort with
-// dependency de-duplication, node removal with renumbering, constant rules).
+// Graph and Model: the value table, node list and host constants.
+//
+// Node order. TopologicalSort yields the dependency order that stays closest
+// to the order in which nodes were added: among the nodes whose producers have
+// all been placed, the one added first goes next (a Kahn walk over a min-heap
+// of positions). A graph that is already in dependency order is left exactly as
+// it is, and independent branches keep their relative order. Error kinds follow
+// the reference's graph (src/ir/graph.cpp): an empty name is InvalidArgument, a
+// duplicate value AlreadyExists, an undefined output NotFound, a cycle
+// InvalidArgument.
 #include "cutriton/ir/graph.h"
 
-#include <deque>
-#include <set>
-#include <unordered_set>
+#include <algorithm>
+#include <functional>
+#include <queue>
 
 #include "cutriton/core/buffer.h"
 
@@ -13,26 +20,23 @@ namespace cutriton {
 
 Status Graph::AddValue(ValueDesc value) {
   if (value.name.empty()) return Status::InvalidArgument("value name must not be empty");
-  const std::string key = value.name;
-  if (!values_.emplace(key, std::move(value)).second) {
-    return Status::AlreadyExists("value already exists: " + key);
-  }
+  auto [slot, fresh] = values_.try_emplace(value.name);
+  if (!fresh) return Status::AlreadyExists("value already exists: " + value.name);
+  slot->second = std::move(value);
   return Status::OK();
 }
 
 Status Graph::AddInput(std::string name, TensorDesc desc) {
   if (name.empty()) return Status::InvalidArgument("input name must not be empty");
-  if (values_.count(name) == 0) {
-    CUTRITON_RETURN_IF_ERROR(AddValue(ValueDesc{name, std::move(desc), false}));
-  } else {
-    CUTRITON_RETURN_IF_ERROR(SetValueDesc(name, std::move(desc)));
-  }
+  ValueDesc& value = values_[name];
+  value.name = name;
+  value.tensor = std::move(desc);
   inputs_.push_back(std::move(name));
   return Status::OK();
 }
 
 Status Graph::AddOutput(std::string name) {
-  if (values_.count(name) == 0) return Status::NotFound("graph output is not a value: " + name);
+  if (FindValue(name) == nullptr) return Status::NotFound("graph output is not a value: " + name);
   outputs_.push_back(std::move(name));
   return Status::OK();
 }
@@ -40,21 +44,22 @@ Status Graph::AddOutput(std::string name) {
 Status Graph::AddNode(Node node) {
   if (node.name().empty()) return Status::InvalidArgument("node name must not be empty");
   if (node.op_type().empty()) return Status::InvalidArgument("node op_type must not be empty");
-  for (const auto& name : node.outputs()) CUTRITON_RETURN_IF_ERROR(EnsureValue(name));
-  for (const auto& name : node.inputs()) CUTRITON_RETURN_IF_ERROR(EnsureValue(name));
+  for (const auto* names : {&node.outputs(), &node.inputs()}) {
+    for (const auto& name : *names) CUTRITON_RETURN_IF_ERROR(EnsureValue(name));
+  }
   node.set_id(static_cast<int>(nodes_.size()));
   nodes_.push_back(std::move(node));
   return Status::OK();
 }
 
 const ValueDesc* Graph::FindValue(const std::string& name) const {
-  const auto it = values_.find(name);
-  return it == values_.end() ? nullptr : &it->second;
+  const auto found = values_.find(name);
+  return found == values_.end() ? nullptr : &found->second;
 }
 
 ValueDesc* Graph::MutableValue(const std::string& name) {
-  const auto it = values_.find(name);
-  return it == values_.end() ? nullptr : &it->second;
+  const auto found = values_.find(name);
+  return found == values_.end() ? nullptr : &found->second;
 }
 
 Status Graph::SetValueDesc(const std::string& name, TensorDesc desc) {
@@ -66,116 +71,131 @@ Status Graph::SetValueDesc(const std::string& name, TensorDesc desc) {
 
 Status Graph::EnsureValue(std::string name, TensorDesc desc) {
   if (name.empty()) return Status::InvalidArgument("value name must not be empty");
-  if (values_.count(name) == 0) {
-    ValueDesc value{name, std::move(desc), false};
-    values_.emplace(std::move(name), std::move(value));
-  }
+  auto [slot, fresh] = values_.try_emplace(name);
+  if (fresh) slot->second = ValueDesc{std::move(name), std::move(desc), false};
   return Status::OK();
 }
 
 std::unordered_map<std::string, int> Graph::BuildProducerMap() const {
-  std::unordered_map<std::string, int> producers;
+  std::unordered_map<std::string, int> producer_of;
   for (const auto& node : nodes_) {
-    for (const auto& name : node.outputs()) producers[name] = node.id();
+    for (const auto& name : node.outputs()) producer_of[name] = node.id();
   }
-  return producers;
+  return producer_of;
 }
 
 std::unordered_map<std::string, std::vector<int>> Graph::BuildConsumerMap() const {
-  std::unordered_map<std::string, std::vector<int>> consumers;
+  std::unordered_map<std::string, std::vector<int>> readers;
   for (const auto& node : nodes_) {
-    for (const auto& name : node.inputs()) consumers[name].push_back(node.id());
+    for (const auto& name : node.inputs()) readers[name].push_back(node.id());
   }
-  return consumers;
+  return readers;
 }
 
 Status Graph::TopologicalSort() {
-  const auto producers = BuildProducerMap();
   const std::size_t count = nodes_.size();
-  std::vector<int> pending(count, 0);
-  std::vector<std::vector<int>> successors(count);
-  for (const auto& node : nodes_) {
-    std::set<int> dependencies;
-    for (const auto& name : node.inputs()) {
-      const auto producer = producers.find(name);
-      if (producer != producers.end() && producer->second != node.id()) {
-        dependencies.insert(producer->second);
+  const auto producer_of = BuildProducerMap();
+  // Per node: the distinct other nodes it reads from (positions), and the
+  // reverse edges used to release readers once a producer is placed.
+  std::vector<int> unplaced_producers(count, 0);
+  std::vector<std::vector<int>> readers(count);
+  for (std::size_t position = 0; position < count; ++position) {
+    std::vector<int> sources;
+    for (const auto& name : nodes_[position].inputs()) {
+      const auto found = producer_of.find(name);
+      if (found != producer_of.end() && found->second != static_cast<int>(position)) {
+        sources.push_back(found->second);
       }
     }
-    pending[static_cast<std::size_t>(node.id())] = static_cast<int>(dependencies.size());
-    for (const int dependency : dependencies) {
-      successors[static_cast<std::size_t>(dependency)].push_back(node.id());
-    }
+    std::sort(sources.begin(), sources.end());
+    sources.erase(std::unique(sources.begin(), sources.end()), sources.end());
+    unplaced_producers[position] = static_cast<int>(sources.size());
+    for (const int source : sources) readers[static_cast<std::size_t>(source)].push_back(static_cast<int>(position));
   }
-  std::deque<int> ready;
-  for (std::size_t i = 0; i < count; ++i) {
-    if (pending[i] == 0) ready.push_back(static_cast<int>(i));
+  std::priority_queue<int, std::vector<int>, std::greater<int>> ready;
+  for (std::size_t position = 0; position < count; ++position) {
+    if (unplaced_producers[position] == 0) ready.push(static_cast<int>(position));
   }
-  std::vector<Node> ordered;
-  ordered.reserve(count);
+  std::vector<int> order;
+  order.reserve(count);
   while (!ready.empty()) {
-    const int id = ready.front();
-    ready.pop_front();
-    ordered.push_back(nodes_[static_cast<std::size_t>(id)]);
-    for (const int next : successors[static_cast<std::size_t>(id)]) {
-      if (--pending[static_cast<std::size_t>(next)] == 0) ready.push_back(next);
+    const int position = ready.top();
+    ready.pop();
+    order.push_back(position);
+    for (const int reader : readers[static_cast<std::size_t>(position)]) {
+      if (--unplaced_producers[static_cast<std::size_t>(reader)] == 0) ready.push(reader);
     }
   }
-  if (ordered.size() != count) return Status::InvalidArgument("graph contains a cycle");
-  nodes_ = std::move(ordered);
+  if (order.size() != count) {
+    std::string stuck;  // nodes on or behind a cycle were never released
+    for (std::size_t position = 0; position < count; ++position) {
+      if (unplaced_producers[position] > 0) stuck += (stuck.empty() ? "" : ", ") + nodes_[position].name();
+    }
+    return Status::InvalidArgument("graph contains a cycle through: " + stuck);
+  }
+  std::vector<Node> placed;
+  placed.reserve(count);
+  for (const int position : order) placed.push_back(std::move(nodes_[static_cast<std::size_t>(position)]));
+  nodes_ = std::move(placed);
   RenumberNodes();
   return Status::OK();
 }
 
 Status Graph::RemoveNodes(const std::vector<int>& node_ids) {
-  const std::unordered_set<int> doomed(node_ids.begin(), node_ids.end());
-  std::vector<Node> kept;
-  kept.reserve(nodes_.size());
-  for (auto& node : nodes_) {
-    if (doomed.count(node.id()) == 0) kept.push_back(std::move(node));
-  }
-  nodes_ = std::move(kept);
+  std::vector<int> doomed = node_ids;
+  std::sort(doomed.begin(), doomed.end());
+  const auto survives = [&](const Node& node) { return !std::binary_search(doomed.begin(), doomed.end(), node.id()); };
+  nodes_.erase(std::stable_partition(nodes_.begin(), nodes_.end(), survives), nodes_.end());
   RenumberNodes();
   return Status::OK();
 }
 
 void Graph::RenumberNodes() {
-  for (std::size_t i = 0; i < nodes_.size(); ++i) nodes_[i].set_id(static_cast<int>(i));
+  int id = 0;
+  for (auto& node : nodes_) node.set_id(id++);
 }
 
 std::vector<int64_t> GetIntListAttribute(const Node& node, const std::string& key,
                                          std::vector<int64_t> fallback) {
-  if (auto value = node.GetAttribute<std::vector<int64_t>>(key)) return *value;
-  return fallback;
+  return node.GetAttribute<std::vector<int64_t>>(key).value_or(std::move(fallback));
 }
 
 int64_t GetIntAttribute(const Node& node, const std::string& key, int64_t fallback) {
-  if (auto value = node.GetAttribute<int64_t>(key)) return *value;
-  return fallback;
+  return node.GetAttribute<int64_t>(key).value_or(fallback);
 }
 
-Status Model::AddConstant(std::string name, Tensor tensor) {
+namespace {
+
+// A model constant is host data that covers its description.
+Status CheckHostConstant(const std::string& name, const Tensor& tensor) {
   if (name.empty()) return Status::InvalidArgument("constant name must not be empty");
   CUTRITON_RETURN_IF_ERROR(tensor.desc().Validate());
-  if (!tensor.defined() || tensor.buffer()->empty()) {
-    return Status::InvalidArgument("constant has no Buffer: " + name);
-  }
-  if (tensor.buffer()->device_type() != DeviceType::kCPU ||
-      tensor.desc().device_type != DeviceType::kCPU) {
-    return Status::InvalidArgument("model constants must live in host memory: " + name);
-  }
-  const std::size_t capacity = tensor.buffer()->size_bytes();
-  if (tensor.byte_offset() > capacity ||
-      tensor.desc().ByteSize() > capacity - tensor.byte_offset()) {
+  const std::shared_ptr<Buffer>& buffer = tensor.buffer();
+  if (buffer == nullptr || buffer->empty()) return Status::InvalidArgument("constant has no Buffer: " + name);
+  const bool on_host = buffer->device_type() == DeviceType::kCPU && tensor.desc().device_type == DeviceType::kCPU;
+  if (!on_host) return Status::InvalidArgument("model constants must live in host memory: " + name);
+  const std::size_t end = tensor.byte_offset() + tensor.desc().ByteSize();
+  if (tensor.byte_offset() > buffer->size_bytes() || end > buffer->size_bytes()) {
     return Status::InvalidArgument("constant Buffer is too small: " + name);
   }
-  if (constants_.count(name) != 0) return Status::AlreadyExists("constant already exists: " + name);
-  if (ValueDesc* existing = graph_.MutableValue(name)) {
-    if (existing->is_constant) return Status::AlreadyExists("constant already exists: " + name);
-    existing->tensor = tensor.desc();
-    existing->is_constant = true;
-  } else {
+  return Status::OK();
+}
+
+}  // namespace
+
+Status Model::AddConstant(std::string name, Tensor tensor) {
+  CUTRITON_RETURN_IF_ERROR(CheckHostConstant(name, tensor));
+  ValueDesc* value = graph_.MutableValue(name);
+  if (constants_.count(name) != 0 || (value != nullptr && value->is_constant)) {
+    return Status::AlreadyExists("constant already exists: " + name);
+  }
+  // A name that nodes already read (declared before its data) becomes the
+  // constant in place.
+  if (value == nullptr) {
     CUTRITON_RETURN_IF_ERROR(graph_.AddValue(ValueDesc{name, tensor.desc(), true}));
+  } else {
+    value->tensor = tensor.desc();
+    value->is_constant = true;
   }
   constants_.emplace(std::move(name), std::move(tensor));
   return Status::OK();

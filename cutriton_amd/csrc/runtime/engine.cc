@@ -1,26 +1,27 @@
-// Engine and ExecutionContext over HIP. Behaviour follows reference
-// src/runtime/engine.cpp:
-//   * EngineState: constants uploaded once, module cache created once
-//     (340-395);
-//   * binding validation (79-110, 404-454), profiles and shape resolution
-//     (462-576), tensor placement in the planned workspace (593-668), kernel
-//     creation (670-723);
-//   * tuner: FNV-1a-64 key over op, tensors, attributes, candidates, artifact
-//     identity, device and driver (215-295); cache files written atomically
-//     (297-335); warm-up, numerical check against candidate 0 (1e-4 FP32,
-//     1e-2 FP16, relative + absolute), median of timed runs (725-891);
-//   * RunAsync: per-op event pairs (event record nodes around per-op child
-//     graphs when capturing), graph
-//     capture keyed by profile, workspace, bound tensors and selected
-//     candidates, LRU eviction of the least recently used graph (925-1079);
-//   * Synchronize: stream sync, then per-op durations into the Profiler
-//     (1081-1119).
-// Two deliberate differences: before timing candidates, the tuner runs the
-// default candidate of every op once, so that intermediate inputs hold the
-// values of the current inputs rather than uninitialised workspace memory;
-// and each timed sample is a back-to-back batch of runs (about 0.2 ms),
-// not one run between synchronisations, whose launch and idle overheads
-// are as large as a short kernel.
+// Engine and ExecutionContext over HIP.
+//
+// An Engine holds the compiled plan and, shared by all its contexts, the
+// device copies of the constants (uploaded once, with re-laid-out copies made
+// on the GPU) and the cache of loaded code objects. An ExecutionContext is one
+// run session: its bindings, its shapes (static, or a point of a shape
+// profile), the tensors of the current run (constants, bindings, and the
+// intermediates placed in its workspace), the selected candidate and kernels
+// of every op, and the HIP state (stream, per-op events, captured graphs).
+//
+// Preparation is lazy and layered: a binding change invalidates the tensor
+// table; a shape change also the kernels and tuning choices (and the
+// bindings, whose shapes no longer fit); a profile change also the workspace
+// and the captured graphs. A run prepares what is stale: tensors, then tuning
+// choices, then kernels; then it replays (or captures) the hipGraph keyed by
+// profile, workspace, bound buffers, shapes and candidates - the key the
+// reference's graph cache uses (src/runtime/engine.cpp:1003-1024), so its
+// least-recently-used eviction behaves alike.
+//
+// The tuner (TuneOnMiss / ForceRetune) first runs the current selection of
+// every op once, so that intermediate inputs hold values derived from the
+// bound inputs, then times every candidate of each op in back-to-back batches
+// of about 0.2 ms, rejects candidates whose output strays from the first
+// candidate's by more than the numeric gate, and records the fastest.
 #include "cutriton/runtime/engine.h"
 
 #include <algorithm>
@@ -30,20 +31,16 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <filesystem>
-#include <fstream>
-#include <iomanip>
 #include <limits>
 #include <mutex>
 #include <optional>
 #include <sstream>
-#include <type_traits>
-#include <variant>
 
 #include "cutriton/core/buffer.h"
 #include "cutriton/ir/pass.h"
 #include "cutriton_hip_runtime.h"
 #include "runtime/relayout.h"
+#include "runtime/tuning_store.h"
 
 namespace cutriton {
 namespace {
@@ -53,68 +50,53 @@ Status RuntimeStatus(int code, const char* operation) {
   return Status::RuntimeError(std::string(operation) + ": " + cth_last_error());
 }
 
-bool Contains(const std::vector<std::string>& names, const std::string& name) {
-  return std::find(names.begin(), names.end(), name) != names.end();
-}
-
-// IEEE binary16 -> binary32 (exact).
-float HalfToFloat(std::uint16_t h) {
-  const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000u) << 16;
-  const std::uint32_t exponent = (h >> 10) & 0x1fu;
-  std::uint32_t mantissa = h & 0x3ffu;
-  std::uint32_t bits;
-  if (exponent == 0x1fu) {
-    bits = sign | 0x7f800000u | (mantissa << 13);
-  } else if (exponent != 0) {
-    bits = sign | ((exponent + 112u) << 23) | (mantissa << 13);
-  } else if (mantissa == 0) {
-    bits = sign;
+// binary16 -> binary32, exact for every input including subnormals.
+float WidenHalf(std::uint16_t bits) {
+  const int exponent = (bits >> 10) & 0x1f;
+  const int fraction = bits & 0x3ff;
+  float magnitude;
+  if (exponent == 0) {
+    magnitude = std::ldexp(static_cast<float>(fraction), -24);
+  } else if (exponent == 0x1f) {
+    magnitude = fraction == 0 ? std::numeric_limits<float>::infinity() : std::numeric_limits<float>::quiet_NaN();
   } else {
-    int shift = 0;
-    while ((mantissa & 0x400u) == 0) {
-      mantissa <<= 1;
-      ++shift;
-    }
-    bits = sign | (static_cast<std::uint32_t>(113 - shift) << 23) | ((mantissa & 0x3ffu) << 13);
+    magnitude = std::ldexp(static_cast<float>(fraction | 0x400), exponent - 25);
   }
-  float value;
-  std::memcpy(&value, &bits, sizeof(value));
-  return value;
+  return (bits & 0x8000) ? -magnitude : magnitude;
 }
 
-Status TensorToHostFloats(const Tensor& tensor, std::vector<float>* out) {
+// The tensor's elements on the host as floats (the tuner's numeric gate).
+Status ReadBackAsFloats(const Tensor& tensor, std::vector<float>* out) {
   const auto count = static_cast<std::size_t>(tensor.desc().NumElements());
-  out->assign(count, 0.0f);
-  if (tensor.desc().dtype == DataType::kFloat32) {
-    return tensor.buffer()->CopyToHost(out->data(), tensor.desc().ByteSize(), tensor.byte_offset());
+  switch (tensor.desc().dtype) {
+    case DataType::kFloat32:
+      out->resize(count);
+      return tensor.buffer()->CopyToHost(out->data(), tensor.desc().ByteSize(), tensor.byte_offset());
+    case DataType::kFloat16: {
+      std::vector<std::uint16_t> bits(count);
+      CUTRITON_RETURN_IF_ERROR(tensor.buffer()->CopyToHost(bits.data(), tensor.desc().ByteSize(), tensor.byte_offset()));
+      out->resize(count);
+      std::transform(bits.begin(), bits.end(), out->begin(), WidenHalf);
+      return Status::OK();
+    }
+    default:
+      return Status::Unsupported("tuning comparison supports float32/float16 only");
   }
-  if (tensor.desc().dtype == DataType::kFloat16) {
-    std::vector<std::uint16_t> halves(count);
-    CUTRITON_RETURN_IF_ERROR(
-        tensor.buffer()->CopyToHost(halves.data(), tensor.desc().ByteSize(), tensor.byte_offset()));
-    for (std::size_t i = 0; i < count; ++i) (*out)[i] = HalfToFloat(halves[i]);
-    return Status::OK();
-  }
-  return Status::Unsupported("tuning comparison supports float32/float16 only");
 }
 
-Status ValidateBoundTensor(const std::string& name, const TensorDesc& expected, const Tensor& tensor) {
+// A caller's tensor for graph value `name`, whose plan description is `want`.
+Status CheckBinding(const std::string& name, const TensorDesc& want, const Tensor& tensor) {
   CUTRITON_RETURN_IF_ERROR(tensor.desc().Validate());
-  if (!tensor.defined() || tensor.buffer()->empty()) {
-    return Status::InvalidArgument("tensor Buffer is not defined: " + name);
-  }
-  const TensorDesc& actual = tensor.desc();
-  if (actual.shape != expected.shape || actual.dtype != expected.dtype ||
-      actual.layout != expected.layout || actual.device_type != expected.device_type ||
-      actual.device_id != expected.device_id) {
-    return Status::InvalidArgument("tensor description does not match the plan: " + name);
-  }
-  if (tensor.buffer()->device_type() != expected.device_type ||
-      tensor.buffer()->device_id() != expected.device_id) {
+  if (!tensor.defined() || tensor.buffer()->empty()) return Status::InvalidArgument("tensor Buffer is not defined: " + name);
+  const TensorDesc& have = tensor.desc();
+  const bool same = have.shape == want.shape && have.dtype == want.dtype && have.layout == want.layout &&
+                    have.device_type == want.device_type && have.device_id == want.device_id;
+  if (!same) return Status::InvalidArgument("tensor description does not match the plan: " + name);
+  const Buffer& buffer = *tensor.buffer();
+  if (buffer.device_type() != want.device_type || buffer.device_id() != want.device_id) {
     return Status::InvalidArgument("tensor Buffer is on another device: " + name);
   }
-  const std::size_t capacity = tensor.buffer()->size_bytes();
-  if (tensor.byte_offset() > capacity || expected.ByteSize() > capacity - tensor.byte_offset()) {
+  if (tensor.byte_offset() > buffer.size_bytes() || want.ByteSize() > buffer.size_bytes() - tensor.byte_offset()) {
     return Status::InvalidArgument("tensor Buffer is too small: " + name);
   }
   return Status::OK();
@@ -175,104 +157,7 @@ Status CreateHipState(int device, std::size_t op_count, bool profiling, HipExecu
   return Status::OK();
 }
 
-std::string TuningKey(const PlanOp& op, const Node& node, const Graph& graph, int device_id) {
-  std::ostringstream m;
-  m << op.op_type << '|' << device_id;
-  auto tensors = [&](const char* role, const std::vector<std::string>& names) {
-    for (const auto& name : names) {
-      m << '|' << role << ':' << name;
-      if (const ValueDesc* v = graph.FindValue(name)) {
-        m << ':' << static_cast<int>(v->tensor.dtype) << ':' << v->tensor.layout;
-        for (const int64_t d : v->tensor.shape) m << ':' << d;
-      }
-    }
-  };
-  tensors("input", op.inputs);
-  tensors("output", op.outputs);
-  std::vector<std::string> keys;
-  for (const auto& attribute : node.attributes()) keys.push_back(attribute.first);
-  std::sort(keys.begin(), keys.end());
-  for (const auto& key : keys) {
-    const Attribute& a = node.attributes().at(key);
-    m << "|attribute:" << key << ':' << a.index();
-    std::visit(
-        [&](const auto& value) {
-          using T = std::decay_t<decltype(value)>;
-          if constexpr (std::is_same_v<T, std::vector<int64_t>> || std::is_same_v<T, std::vector<double>>) {
-            for (const auto item : value) m << ':' << item;
-          } else {
-            m << ':' << value;
-          }
-        },
-        a);
-  }
-  for (const auto& candidate : op.candidates) {
-    m << '|' << candidate.candidate_id;
-    for (const auto& step : candidate.steps) {
-      if (const auto* inv = std::get_if<KernelInvocation>(&step)) {
-        const KernelArtifact& a = inv->artifact;
-        m << "|pack:" << a.pack_name << ':' << a.pack_version << "|kernel:" << a.kernel_id << ':'
-          << a.kernel_version << ':' << a.variant_id << "|abi:" << a.abi_schema_version
-          << "|generator:" << a.generator_version << "|toolchain:" << a.triton_version
-          << "|code:" << a.sha256;
-      } else {
-        m << "|view";
-      }
-    }
-  }
-  cth_device_info info;
-  if (cth_device_query(device_id, &info) == 0) {
-    m << "|arch:" << info.arch_name << "|cu:" << info.compute_units << "|uuid:";
-    for (const unsigned char byte : info.uuid) m << std::hex << static_cast<int>(byte) << std::dec;
-    m << "|driver:" << info.driver_version << "|runtime:" << info.runtime_version;
-  }
-  std::uint64_t hash = 0xcbf29ce484222325ull;  // FNV-1a 64 offset basis
-  for (const unsigned char c : m.str()) {
-    hash ^= c;
-    hash *= 0x100000001b3ull;  // FNV-1a 64 prime
-  }
-  std::ostringstream hex;
-  hex << std::hex << std::setw(16) << std::setfill('0') << hash;
-  return hex.str();
-}
-
-std::optional<std::string> ReadTuningChoice(const std::filesystem::path& path) {
-  std::ifstream in(path);
-  if (!in) return std::nullopt;
-  std::ostringstream contents;
-  contents << in.rdbuf();
-  const std::string text = contents.str();
-  const std::string marker = "\"candidate_id\": \"";
-  const auto begin = text.find(marker);
-  if (begin == std::string::npos) return std::nullopt;
-  const auto first = begin + marker.size();
-  const auto last = text.find('"', first);
-  if (last == std::string::npos) return std::nullopt;
-  return text.substr(first, last - first);
-}
-
-Status WriteTuningChoice(const std::filesystem::path& path, const std::string& key,
-                         const std::string& candidate_id, double median_ms) {
-  std::error_code error;
-  std::filesystem::create_directories(path.parent_path(), error);
-  if (error) return Status::RuntimeError("cannot create the tuning cache directory: " + error.message());
-  const std::string staging = path.string() + ".tmp";
-  {
-    std::ofstream out(staging, std::ios::trunc);
-    out << "{\n  \"schema_version\": 1,\n  \"tuning_key\": \"" << key << "\",\n  \"candidate_id\": \""
-        << candidate_id << "\",\n  \"median_ms\": " << median_ms << "\n}\n";
-    if (!out) return Status::RuntimeError("cannot write the tuning cache");
-  }
-  std::filesystem::rename(staging, path, error);
-  if (error) {
-    std::filesystem::remove(path, error);
-    error.clear();
-    std::filesystem::rename(staging, path, error);
-  }
-  return error ? Status::RuntimeError("cannot publish the tuning cache: " + error.message()) : Status::OK();
-}
-
-std::optional<std::size_t> FindCandidate(const PlanOp& op, const std::string& id) {
+std::optional<std::size_t> CandidateIndex(const PlanOp& op, const std::string& id) {
   for (std::size_t i = 0; i < op.candidates.size(); ++i) {
     if (op.candidates[i].candidate_id == id) return i;
   }
@@ -304,9 +189,13 @@ class EngineState {
   explicit EngineState(ExecutablePlan p) : plan(std::move(p)) {}
 
   Status InitializeConstants() {
-    std::call_once(constants_once_, [&] { constants_status_ = UploadConstants(); });
+    std::call_once(constants_once_, [&] {
+      constants_status_ = UploadConstants();
+      constants_ready_ = constants_status_.ok();
+    });
     return constants_status_;
   }
+  bool ConstantsReady() const { return constants_ready_; }
 
   Status InitializeModuleCache() {
     if (plan.backend_options().device.type != DeviceType::kHIP) return Status::OK();
@@ -401,6 +290,7 @@ class EngineState {
 
   std::once_flag constants_once_;
   Status constants_status_;
+  bool constants_ready_{false};
   std::once_flag module_once_;
   Status module_status_;
 };
@@ -414,13 +304,13 @@ std::unique_ptr<ExecutionContext> Engine::CreateExecutionContext() const {
 }
 
 ExecutionContext::ExecutionContext(std::shared_ptr<EngineState> state) : state_(std::move(state)) {
-  if (state_ != nullptr && state_->plan.profile_plans().size() == 1) {
-    selected_profile_ = 0;
-    const ProfilePlan& pp = state_->plan.profile_plans().front();
-    resolved_graph_ = pp.opt_graph;
-    shapes_resolved_ = true;
-    for (const auto& entry : pp.profile.inputs) input_shapes_[entry.first] = entry.second.opt;
-  }
+  // A plan with exactly one profile starts on it, at its opt shapes.
+  if (state_ == nullptr || state_->plan.profile_plans().size() != 1) return;
+  const ProfilePlan& only = state_->plan.profile_plans().front();
+  selected_profile_ = 0;
+  for (const auto& [input, range] : only.profile.inputs) input_shapes_[input] = range.opt;
+  resolved_graph_ = only.opt_graph;
+  shapes_resolved_ = true;
 }
 
 ExecutionContext::~ExecutionContext() {
@@ -428,15 +318,26 @@ ExecutionContext::~ExecutionContext() {
   DestroyHipState(static_cast<HipExecutionState*>(hip_state_));
 }
 
-const Graph& ExecutionContext::ActiveGraph() const {
-  return shapes_resolved_ ? resolved_graph_ : state_->plan.graph();
+// Captured graphs survive binding and shape changes: their keys name the
+// bound buffers, shapes and candidates, so a later run with the same
+// bindings replays its graph again (least recently used evicted first).
+void ExecutionContext::Invalidate(Stale what) {
+  tensors_prepared_ = false;
+  if (what == Stale::kBindings) return;
+  bound_.clear();
+  kernels_.clear();
+  kernels_prepared_ = false;
+  tuning_prepared_ = false;
+  if (what == Stale::kShapes) return;
+  workspace_.reset();
+  InvalidateHipGraph();
 }
 
+const Graph& ExecutionContext::ActiveGraph() const { return shapes_resolved_ ? resolved_graph_ : state_->plan.graph(); }
+
 const MemoryPlan& ExecutionContext::ActiveMemoryPlan() const {
-  if (selected_profile_ >= 0) {
-    return state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).max_memory_plan;
-  }
-  return state_->plan.memory_plan();
+  if (selected_profile_ < 0) return state_->plan.memory_plan();
+  return state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).max_memory_plan;
 }
 
 Status ExecutionContext::BindInput(const std::string& name, Tensor tensor) {
@@ -445,13 +346,13 @@ Status ExecutionContext::BindInput(const std::string& name, Tensor tensor) {
   if (!state_->plan.profile_plans().empty() && !shapes_resolved_) {
     return Status::RuntimeError("ResolveShapes must be called before binding");
   }
-  const Graph& graph = ActiveGraph();
-  if (!Contains(graph.inputs(), name)) return Status::NotFound("name is not a graph input: " + name);
-  const ValueDesc* value = graph.FindValue(name);
+  const auto& inputs = ActiveGraph().inputs();
+  const ValueDesc* value = ActiveGraph().FindValue(name);
+  if (std::find(inputs.begin(), inputs.end(), name) == inputs.end()) return Status::NotFound("name is not a graph input: " + name);
   if (value == nullptr) return Status::NotFound("graph input description is missing: " + name);
-  CUTRITON_RETURN_IF_ERROR(ValidateBoundTensor(name, value->tensor, tensor));
-  tensors_[name] = std::move(tensor);
-  tensors_prepared_ = false;
+  CUTRITON_RETURN_IF_ERROR(CheckBinding(name, value->tensor, tensor));
+  bound_[name] = std::move(tensor);
+  Invalidate(Stale::kBindings);
   return Status::OK();
 }
 
@@ -461,74 +362,61 @@ Status ExecutionContext::BindOutput(const std::string& name, Tensor tensor) {
   if (!state_->plan.profile_plans().empty() && !shapes_resolved_) {
     return Status::RuntimeError("ResolveShapes must be called before binding");
   }
-  const Graph& graph = ActiveGraph();
-  if (!Contains(graph.outputs(), name)) return Status::NotFound("name is not a graph output: " + name);
-  const ValueDesc* value = graph.FindValue(name);
+  const auto& outputs = ActiveGraph().outputs();
+  const ValueDesc* value = ActiveGraph().FindValue(name);
+  if (std::find(outputs.begin(), outputs.end(), name) == outputs.end()) return Status::NotFound("name is not a graph output: " + name);
   if (value == nullptr) return Status::NotFound("graph output description is missing: " + name);
-  CUTRITON_RETURN_IF_ERROR(ValidateBoundTensor(name, value->tensor, tensor));
-  tensors_[name] = std::move(tensor);
-  tensors_prepared_ = false;
+  CUTRITON_RETURN_IF_ERROR(CheckBinding(name, value->tensor, tensor));
+  bound_[name] = std::move(tensor);
+  Invalidate(Stale::kBindings);
   return Status::OK();
 }
 
 Status ExecutionContext::SelectShapeProfile(const std::string& name) {
   if (run_pending_) return Status::RuntimeError("cannot change the profile while a run is pending");
   const auto& profiles = state_->plan.profile_plans();
-  const auto found = std::find_if(profiles.begin(), profiles.end(),
-                                  [&](const ProfilePlan& p) { return p.profile.name == name; });
+  const auto found = std::find_if(profiles.begin(), profiles.end(), [&](const ProfilePlan& p) { return p.profile.name == name; });
   if (found == profiles.end()) return Status::NotFound("ShapeProfile is not defined: " + name);
   selected_profile_ = static_cast<int>(found - profiles.begin());
   input_shapes_.clear();
-  for (const auto& entry : found->profile.inputs) input_shapes_[entry.first] = entry.second.opt;
+  for (const auto& [input, range] : found->profile.inputs) input_shapes_[input] = range.opt;
   resolved_graph_ = found->opt_graph;
   shapes_resolved_ = true;
-  tensors_.clear();
-  workspace_.reset();
-  tensors_prepared_ = false;
-  kernels_.clear();
-  kernels_prepared_ = false;
-  tuning_prepared_ = false;
-  InvalidateHipGraph();
+  Invalidate(Stale::kProfile);
   return Status::OK();
 }
 
 Status ExecutionContext::SetInputShape(const std::string& name, std::vector<int64_t> shape) {
   if (run_pending_) return Status::RuntimeError("cannot change a shape while a run is pending");
   if (selected_profile_ < 0) return Status::RuntimeError("select a ShapeProfile before setting shapes");
-  const ShapeProfile& profile =
-      state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).profile;
+  const ShapeProfile& profile = state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).profile;
   const auto range = profile.inputs.find(name);
   if (range == profile.inputs.end()) return Status::NotFound("name is not a profiled graph input: " + name);
-  if (shape.size() != range->second.min.size()) {
-    return Status::ShapeError("input rank does not match the profile: " + name);
-  }
+  const ShapeRange& r = range->second;
+  if (shape.size() != r.min.size()) return Status::ShapeError("input rank does not match the profile: " + name);
   for (std::size_t axis = 0; axis < shape.size(); ++axis) {
-    if (shape[axis] < range->second.min[axis] || shape[axis] > range->second.max[axis]) {
+    if (shape[axis] < r.min[axis] || shape[axis] > r.max[axis]) {
       return Status::ShapeError("input shape is outside the profile range: " + name);
     }
   }
   input_shapes_[name] = std::move(shape);
   shapes_resolved_ = false;
-  tensors_.clear();
-  tensors_prepared_ = false;
-  kernels_.clear();
-  kernels_prepared_ = false;
-  tuning_prepared_ = false;
+  Invalidate(Stale::kShapes);
   return Status::OK();
 }
 
 Status ExecutionContext::ResolveShapes() {
   if (selected_profile_ < 0) return Status::RuntimeError("select a ShapeProfile before resolving shapes");
-  const ProfilePlan& pp = state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_));
-  resolved_graph_ = pp.opt_graph;
-  for (const auto& input : resolved_graph_.inputs()) {
+  Graph graph = state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).opt_graph;
+  for (const auto& input : graph.inputs()) {
     const auto shape = input_shapes_.find(input);
     if (shape == input_shapes_.end()) return Status::InvalidArgument("input shape is not set: " + input);
-    TensorDesc desc = resolved_graph_.FindValue(input)->tensor;
+    TensorDesc desc = graph.FindValue(input)->tensor;
     desc.shape = shape->second;
-    CUTRITON_RETURN_IF_ERROR(resolved_graph_.SetValueDesc(input, std::move(desc)));
+    CUTRITON_RETURN_IF_ERROR(graph.SetValueDesc(input, std::move(desc)));
   }
-  CUTRITON_RETURN_IF_ERROR(CreateShapeInferencePass()->Run(&resolved_graph_));
+  CUTRITON_RETURN_IF_ERROR(CreateShapeInferencePass()->Run(&graph));
+  resolved_graph_ = std::move(graph);
   shapes_resolved_ = true;
   return Status::OK();
 }
@@ -548,123 +436,138 @@ std::size_t ExecutionContext::loaded_cuda_module_count() const {
   return state_ == nullptr ? 0 : LoadedModuleCount(state_->module_cache);
 }
 
-Status ExecutionContext::PrepareTensors() {
+// The largest runtime scratch any candidate declares (tuning may run each).
+std::size_t ExecutionContext::RuntimeScratchNeed() const {
+  std::size_t need = 0;
+  for (const auto& op : state_->plan.ops()) {
+    for (const auto& candidate : op.candidates) {
+      for (const auto& step : candidate.steps) {
+        if (const auto* inv = std::get_if<KernelInvocation>(&step)) {
+          need = std::max(need, static_cast<std::size_t>(std::max<int64_t>(0, inv->artifact.runtime_scratch_bytes)));
+        }
+      }
+    }
+  }
+  return need;
+}
+
+// The run's tensor table: device constants, the caller's bindings, and every
+// planned intermediate (values, Flatten views, candidate temporaries) at its
+// workspace offset.
+Status ExecutionContext::PrepareTensors(bool may_allocate) {
   if (tensors_prepared_) return Status::OK();
   if (state_ == nullptr) return Status::InvalidArgument("ExecutionContext has no EngineState");
+  if (!may_allocate && !state_->ConstantsReady()) {
+    return Status::RuntimeError("constants are not on the device yet: run the context once with RunAsync first");
+  }
   CUTRITON_RETURN_IF_ERROR(state_->InitializeConstants());
-  for (const auto& entry : state_->device_constants) tensors_[entry.first] = entry.second;
-  const MemoryPlan& memory = ActiveMemoryPlan();
   const Device& device = state_->plan.backend_options().device;
-  if (memory.workspace_size_bytes != 0 &&
-      (workspace_ == nullptr || workspace_->size_bytes() < memory.workspace_size_bytes)) {
+  const MemoryPlan& memory = ActiveMemoryPlan();
+  const bool workspace_short = workspace_ == nullptr || workspace_->size_bytes() < memory.workspace_size_bytes;
+  if (memory.workspace_size_bytes != 0 && workspace_short) {
+    if (!may_allocate) {
+      return Status::RuntimeError("the context has no workspace of " + std::to_string(memory.workspace_size_bytes) +
+                                  " bytes: run it once with RunAsync first");
+    }
     if (device.type == DeviceType::kHIP) {
       CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(memory.workspace_size_bytes, device.id, &workspace_));
     } else {
       workspace_ = Buffer::AllocateHost(memory.workspace_size_bytes);
     }
   }
+
+  std::unordered_map<std::string, Tensor> table = state_->device_constants;
+  for (const auto& [name, tensor] : bound_) table[name] = tensor;
+  // Temporaries are described like the value their candidate names.
+  std::unordered_map<std::string, std::string> temporary_like;
+  for (const auto& op : state_->plan.ops()) {
+    for (const auto& candidate : op.candidates) {
+      for (const auto& temporary : candidate.temporaries) temporary_like.emplace(temporary.name, temporary.like_value);
+    }
+  }
   const Graph& graph = ActiveGraph();
-  for (const auto& allocation : memory.allocations) {
+  for (const Allocation& allocation : memory.allocations) {
     const ValueDesc* value = graph.FindValue(allocation.value_name);
     if (value == nullptr) {
-      // A candidate temporary: described like its "like" value.
-      const ValueDesc* like = nullptr;
-      for (const auto& op : state_->plan.ops()) {
-        for (const auto& candidate : op.candidates) {
-          for (const auto& temporary : candidate.temporaries) {
-            if (temporary.name == allocation.value_name) like = graph.FindValue(temporary.like_value);
-          }
-          if (like != nullptr) break;
-        }
-        if (like != nullptr) break;
-      }
-      if (like == nullptr) return Status::Internal("allocation references an unknown value: " + allocation.value_name);
-      tensors_[allocation.value_name] = Tensor(like->tensor, workspace_, allocation.offset);
-      continue;
+      const auto like = temporary_like.find(allocation.value_name);
+      value = like == temporary_like.end() ? nullptr : graph.FindValue(like->second);
+      if (value == nullptr) return Status::Internal("allocation references an unknown value: " + allocation.value_name);
     }
     if (!allocation.alias_of.empty()) {
-      const auto source = tensors_.find(allocation.alias_of);
-      if (source == tensors_.end()) {
-        return Status::Internal("alias source tensor is missing: " + allocation.alias_of);
-      }
+      const auto source = table.find(allocation.alias_of);
+      if (source == table.end()) return Status::Internal("alias source tensor is missing: " + allocation.alias_of);
       if (value->tensor.ByteSize() != source->second.desc().ByteSize()) {
         return Status::ShapeError("alias changes the byte size of " + allocation.value_name);
       }
-      tensors_[allocation.value_name] =
-          Tensor(value->tensor, source->second.buffer(), source->second.byte_offset());
+      table[allocation.value_name] = Tensor(value->tensor, source->second.buffer(), source->second.byte_offset());
       continue;
     }
+    const std::size_t bytes = value->tensor.ByteSize();
     if (workspace_ == nullptr || allocation.offset > workspace_->size_bytes() ||
-        allocation.size_bytes > workspace_->size_bytes() - allocation.offset) {
+        bytes > workspace_->size_bytes() - allocation.offset) {
       return Status::Internal("allocation exceeds the workspace: " + allocation.value_name);
     }
-    tensors_[allocation.value_name] = Tensor(value->tensor, workspace_, allocation.offset);
+    table[allocation.value_name] = Tensor(value->tensor, workspace_, allocation.offset);
   }
-  // One zero-initialised runtime scratch buffer per context, sized for the
-  // largest declared need of any candidate (tuning may run every one).
-  std::int64_t scratch = 0;
-  for (const auto& op : state_->plan.ops()) {
-    for (const auto& candidate : op.candidates) {
-      for (const auto& step : candidate.steps) {
-        if (const auto* inv = std::get_if<KernelInvocation>(&step)) {
-          scratch = std::max(scratch, inv->artifact.runtime_scratch_bytes);
-        }
-      }
-    }
-  }
-  if (scratch > 0 && device.type == DeviceType::kHIP &&
-      (runtime_scratch_ == nullptr || runtime_scratch_->size_bytes() < static_cast<std::size_t>(scratch))) {
-    CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(static_cast<std::size_t>(scratch), device.id, &runtime_scratch_));
-    CUTRITON_RETURN_IF_ERROR(RuntimeStatus(
-        cth_memset(runtime_scratch_->data(), 0, runtime_scratch_->size_bytes(), device.id), "hipMemset"));
+  tensors_ = std::move(table);
+
+  const std::size_t scratch = RuntimeScratchNeed();
+  const bool scratch_short = runtime_scratch_ == nullptr || runtime_scratch_->size_bytes() < scratch;
+  if (may_allocate && scratch > 0 && device.type == DeviceType::kHIP && scratch_short) {
+    CUTRITON_RETURN_IF_ERROR(Buffer::AllocateHip(scratch, device.id, &runtime_scratch_));
+    CUTRITON_RETURN_IF_ERROR(
+        RuntimeStatus(cth_memset(runtime_scratch_->data(), 0, runtime_scratch_->size_bytes(), device.id), "hipMemset"));
     InvalidateHipGraph();
   }
   tensors_prepared_ = true;
   return Status::OK();
 }
 
-Status ExecutionContext::PrepareKernels() {
+Status ExecutionContext::PrepareKernels(bool may_load) {
   if (kernels_prepared_) return Status::OK();
   if (state_ == nullptr) return Status::InvalidArgument("ExecutionContext has no EngineState");
   CUTRITON_RETURN_IF_ERROR(RegisterBuiltinBackends());
   CUTRITON_RETURN_IF_ERROR(state_->InitializeModuleCache());
-  if (selected_candidates_.size() != state_->plan.ops().size()) {
-    return Status::Internal("tuning selections are not prepared");
-  }
-  kernels_.clear();
-  const int device_id = state_->plan.backend_options().device.id;
-  for (std::size_t i = 0; i < state_->plan.ops().size(); ++i) {
-    const PlanOp& op = state_->plan.ops()[i];
+  const auto& ops = state_->plan.ops();
+  if (selected_candidates_.size() != ops.size()) return Status::Internal("tuning selections are not prepared");
+  const BackendOptions& options = state_->plan.backend_options();
+  std::vector<std::vector<std::unique_ptr<OpKernel>>> kernels;
+  for (std::size_t i = 0; i < ops.size(); ++i) {
+    const PlanOp& op = ops[i];
     auto backend = KernelRegistry::Global().GetBackend(op.backend_name);
     if (backend == nullptr) return Status::NotFound("backend is not registered: " + op.backend_name);
     const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
-    const std::size_t selected = selected_candidates_[i];
-    if (selected >= op.candidates.size()) return Status::Internal("selected candidate is out of range");
+    if (selected_candidates_[i] >= op.candidates.size()) return Status::Internal("selected candidate is out of range");
+    const ExecutionCandidate& chosen = op.candidates[selected_candidates_[i]];
     std::vector<std::unique_ptr<OpKernel>> group;
-    for (const auto& step : op.candidates[selected].steps) {
+    for (const auto& step : chosen.steps) {
       std::unique_ptr<OpKernel> kernel;
       if (const auto* inv = std::get_if<KernelInvocation>(&step)) {
-        CUTRITON_RETURN_IF_ERROR(CreateInvocationKernel(*inv, device_id, state_->module_cache, &kernel));
+        if (!may_load && !CodeObjectLoaded(state_->module_cache, inv->artifact)) {
+          return Status::RuntimeError("code object of " + inv->artifact.identity() +
+                                      " is not loaded: run the context once with RunAsync first");
+        }
+        CUTRITON_RETURN_IF_ERROR(CreateInvocationKernel(*inv, options.device.id, state_->module_cache, &kernel));
       } else {
-        CUTRITON_RETURN_IF_ERROR(
-            backend->CreateKernel(node, ActiveGraph(), state_->plan.backend_options(), &kernel));
+        CUTRITON_RETURN_IF_ERROR(backend->CreateKernel(node, ActiveGraph(), options, &kernel));
       }
       if (kernel == nullptr) return Status::Internal("backend returned a null OpKernel");
       group.push_back(std::move(kernel));
     }
-    if (group.empty()) {
+    if (group.empty()) {  // a legacy candidate: the backend's own kernel
       std::unique_ptr<OpKernel> kernel;
-      CUTRITON_RETURN_IF_ERROR(backend->CreateKernel(node, ActiveGraph(), state_->plan.backend_options(), &kernel));
+      CUTRITON_RETURN_IF_ERROR(backend->CreateKernel(node, ActiveGraph(), options, &kernel));
       if (kernel == nullptr) return Status::Internal("backend returned a null OpKernel");
       group.push_back(std::move(kernel));
     }
-    kernels_.push_back(std::move(group));
+    kernels.push_back(std::move(group));
   }
+  kernels_ = std::move(kernels);
   kernels_prepared_ = true;
   return Status::OK();
 }
 
-Status ExecutionContext::PrepareTuning() {
+Status ExecutionContext::PrepareTuning(bool may_time) {
   if (tuning_prepared_) return Status::OK();
   const auto& ops = state_->plan.ops();
   selected_candidates_.clear();
@@ -677,33 +580,28 @@ Status ExecutionContext::PrepareTuning() {
   }
   CUTRITON_RETURN_IF_ERROR(state_->InitializeModuleCache());
   const Graph& graph = ActiveGraph();
+  const TuningStore store(config.cache_dir);
 
-  // Resolve from the cache first; remember which ops still need timing.
+  // Resolve from the store first; collect the ops that still need timing.
+  // Under UseCache a shape that was never tuned takes the profile opt
+  // point's choice.
   std::vector<std::size_t> to_tune;
   std::vector<std::string> keys(ops.size());
   for (std::size_t i = 0; i < ops.size(); ++i) {
     const PlanOp& op = ops[i];
     if (op.candidates.size() < 2) continue;
     const Node& node = graph.nodes().at(static_cast<std::size_t>(op.node_id));
-    keys[i] = TuningKey(op, node, graph, device.id);
+    keys[i] = TuningDecisionKey(op, node, graph, device.id);
     if (config.mode != TuningMode::kForceRetune) {
-      const auto cached = ReadTuningChoice(std::filesystem::path(config.cache_dir) / (keys[i] + ".json"));
-      if (cached) {
-        if (const auto index = FindCandidate(op, *cached)) {
+      std::optional<std::string> recorded = store.Lookup(keys[i]);
+      if (!recorded && config.mode == TuningMode::kUseCache && selected_profile_ >= 0) {
+        const Graph& opt = state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).opt_graph;
+        recorded = store.Lookup(TuningDecisionKey(op, opt.nodes().at(static_cast<std::size_t>(op.node_id)), opt, device.id));
+      }
+      if (recorded) {
+        if (const auto index = CandidateIndex(op, *recorded)) {
           selected_candidates_[i] = *index;
           continue;
-        }
-      }
-      if (config.mode == TuningMode::kUseCache && selected_profile_ >= 0) {
-        const Graph& opt = state_->plan.profile_plans().at(static_cast<std::size_t>(selected_profile_)).opt_graph;
-        const std::string opt_key =
-            TuningKey(op, opt.nodes().at(static_cast<std::size_t>(op.node_id)), opt, device.id);
-        const auto choice = ReadTuningChoice(std::filesystem::path(config.cache_dir) / (opt_key + ".json"));
-        if (choice) {
-          if (const auto index = FindCandidate(op, *choice)) {
-            selected_candidates_[i] = *index;
-            continue;
-          }
         }
       }
     }
@@ -712,6 +610,10 @@ Status ExecutionContext::PrepareTuning() {
   if (to_tune.empty()) {
     tuning_prepared_ = true;
     return Status::OK();
+  }
+  if (!may_time) {
+    return Status::RuntimeError(std::to_string(to_tune.size()) + " ops need tuning (" + ops[to_tune.front()].node_name +
+                                " first): run the context once with RunAsync first");
   }
 
   cth_stream stream = nullptr;
@@ -730,9 +632,10 @@ Status ExecutionContext::PrepareTuning() {
   } cleanup{&stream, &start, &end};
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_create(&start), "hipEventCreate"));
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_create(&end), "hipEventCreate"));
+  void* scratch = runtime_scratch_ ? runtime_scratch_->data() : nullptr;
+  const std::size_t scratch_bytes = runtime_scratch_ ? runtime_scratch_->size_bytes() : 0;
 
-  auto build_kernels = [&](const ExecutionCandidate& candidate,
-                           std::vector<std::unique_ptr<OpKernel>>* out) -> Status {
+  auto build_kernels = [&](const ExecutionCandidate& candidate, std::vector<std::unique_ptr<OpKernel>>* out) -> Status {
     out->clear();
     for (const auto& step : candidate.steps) {
       const auto* inv = std::get_if<KernelInvocation>(&step);
@@ -750,7 +653,7 @@ Status ExecutionContext::PrepareTuning() {
     const Node& node = graph.nodes().at(static_cast<std::size_t>(ops[i].node_id));
     std::vector<std::unique_ptr<OpKernel>> kernels;
     CUTRITON_RETURN_IF_ERROR(build_kernels(ops[i].candidates[selected_candidates_[i]], &kernels));
-    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
+    KernelContext context{&node, &tensors_, stream, nullptr, scratch, scratch_bytes};
     for (auto& kernel : kernels) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
   }
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(stream), "hipStreamSynchronize"));
@@ -761,7 +664,7 @@ Status ExecutionContext::PrepareTuning() {
   for (const std::size_t op_index : to_tune) {
     const PlanOp& op = ops[op_index];
     const Node& node = graph.nodes().at(static_cast<std::size_t>(op.node_id));
-    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
+    KernelContext context{&node, &tensors_, stream, nullptr, scratch, scratch_bytes};
     double best_ms = std::numeric_limits<double>::infinity();
     std::size_t best = op.selected_candidate;
     std::vector<float> reference;
@@ -776,7 +679,7 @@ Status ExecutionContext::PrepareTuning() {
       CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(stream), "hipStreamSynchronize"));
       const Tensor& output = tensors_.at(op.outputs.front());
       std::vector<float> produced;
-      CUTRITON_RETURN_IF_ERROR(TensorToHostFloats(output, &produced));
+      CUTRITON_RETURN_IF_ERROR(ReadBackAsFloats(output, &produced));
       if (reference.empty()) {
         reference = std::move(produced);
         double sum_sq = 0.0;
@@ -840,17 +743,14 @@ Status ExecutionContext::PrepareTuning() {
         best = c;
       }
     }
-    if (!std::isfinite(best_ms)) {
-      return Status::RuntimeError("no numerically valid tuning candidate for " + op.node_name);
-    }
+    if (!std::isfinite(best_ms)) return Status::RuntimeError("no numerically valid tuning candidate for " + op.node_name);
     selected_candidates_[op_index] = best;
     // Leave the op's output as the chosen candidate computes it.
     std::vector<std::unique_ptr<OpKernel>> kernels;
     CUTRITON_RETURN_IF_ERROR(build_kernels(op.candidates[best], &kernels));
     for (auto& kernel : kernels) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(stream), "hipStreamSynchronize"));
-    CUTRITON_RETURN_IF_ERROR(WriteTuningChoice(std::filesystem::path(config.cache_dir) / (keys[op_index] + ".json"),
-                                               keys[op_index], op.candidates[best].candidate_id, best_ms));
+    CUTRITON_RETURN_IF_ERROR(store.Record(keys[op_index], op.candidates[best].candidate_id, best_ms));
   }
   tuning_prepared_ = true;
   return Status::OK();
@@ -858,18 +758,16 @@ Status ExecutionContext::PrepareTuning() {
 
 Status ExecutionContext::ValidateBindings() const {
   const Graph& graph = ActiveGraph();
-  for (const auto& name : graph.inputs()) {
-    if (tensors_.count(name) == 0) return Status::InvalidArgument("graph input is not bound: " + name);
-  }
-  for (const auto& name : graph.outputs()) {
-    if (tensors_.count(name) == 0) return Status::InvalidArgument("graph output is not bound: " + name);
+  for (const auto* names : {&graph.inputs(), &graph.outputs()}) {
+    for (const auto& name : *names) {
+      if (bound_.count(name) == 0) return Status::InvalidArgument("graph value is not bound: " + name);
+    }
   }
   for (const auto& node : graph.nodes()) {
-    for (const auto& name : node.inputs()) {
-      if (tensors_.count(name) == 0) return Status::InvalidArgument("node input tensor is missing: " + name);
-    }
-    for (const auto& name : node.outputs()) {
-      if (tensors_.count(name) == 0) return Status::InvalidArgument("node output tensor is missing: " + name);
+    for (const auto* names : {&node.inputs(), &node.outputs()}) {
+      for (const auto& name : *names) {
+        if (tensors_.count(name) == 0) return Status::InvalidArgument("node tensor is missing: " + name);
+      }
     }
   }
   return Status::OK();
@@ -880,19 +778,19 @@ Status ExecutionContext::Run() {
   return Synchronize();
 }
 
-Status ExecutionContext::EnqueueOps(void* stream, bool capture) {
+Status ExecutionContext::EnqueueOps(void* stream, bool capture, void* scratch, std::size_t scratch_bytes) {
   auto* hip = static_cast<HipExecutionState*>(hip_state_);
-  const bool profiling = state_->plan.enable_profiling();
+  const bool profiling = state_->plan.enable_profiling() && hip != nullptr;
   for (std::size_t i = 0; i < kernels_.size(); ++i) {
     const PlanOp& op = state_->plan.ops()[i];
     const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
-    EventPair& events = hip->events[i];
     // Events inside a capture are graph nodes placed by CaptureGraph.
-    events.timed = profiling && node.op_type() != "Flatten";
-    if (events.timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(events.start, stream), "hipEventRecord"));
-    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
+    const bool timed = profiling && node.op_type() != "Flatten";
+    if (hip != nullptr) hip->events[i].timed = timed;
+    if (timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(hip->events[i].start, stream), "hipEventRecord"));
+    KernelContext context{&node, &tensors_, stream, nullptr, scratch, scratch_bytes};
     for (auto& kernel : kernels_[i]) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
-    if (events.timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(events.end, stream), "hipEventRecord"));
+    if (timed && !capture) CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_event_record(hip->events[i].end, stream), "hipEventRecord"));
   }
   return Status::OK();
 }
@@ -905,9 +803,11 @@ Status ExecutionContext::EnqueueOps(void* stream, bool capture) {
 Status ExecutionContext::CaptureGraph(void* stream, void** exec) {
   auto* hip = static_cast<HipExecutionState*>(hip_state_);
   *exec = nullptr;
+  void* scratch = runtime_scratch_ ? runtime_scratch_->data() : nullptr;
+  const std::size_t scratch_bytes = runtime_scratch_ ? runtime_scratch_->size_bytes() : 0;
   if (!state_->plan.enable_profiling()) {
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_begin_capture(stream), "hipStreamBeginCapture"));
-    const Status enqueued = EnqueueOps(stream, true);
+    const Status enqueued = EnqueueOps(stream, true, scratch, scratch_bytes);
     cth_graph graph = nullptr;
     const Status ended = RuntimeStatus(cth_stream_end_capture(stream, &graph), "hipStreamEndCapture");
     if (!enqueued.ok()) {
@@ -934,7 +834,7 @@ Status ExecutionContext::CaptureGraph(void* stream, void** exec) {
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_graph_add_event_record(parent, previous, events.start, &previous),
                                            "hipGraphAddEventRecordNode"));
     CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_begin_capture(stream), "hipStreamBeginCapture"));
-    KernelContext context{&node, &tensors_, stream, nullptr, ScratchPointer(), ScratchBytes()};
+    KernelContext context{&node, &tensors_, stream, nullptr, scratch, scratch_bytes};
     Status launched = Status::OK();
     for (auto& kernel : kernels_[i]) {
       launched = kernel->Compute(&context);
@@ -961,17 +861,19 @@ Status ExecutionContext::RunAsync(void* stream) {
   if (run_pending_) return Status::RuntimeError("a run is already pending");
   {
     StageTimer timer("tensors");
-    CUTRITON_RETURN_IF_ERROR(PrepareTensors());
+    CUTRITON_RETURN_IF_ERROR(PrepareTensors(true));
   }
   CUTRITON_RETURN_IF_ERROR(ValidateBindings());
   {
     StageTimer timer("tuning");
-    CUTRITON_RETURN_IF_ERROR(PrepareTuning());
+    CUTRITON_RETURN_IF_ERROR(PrepareTuning(true));
   }
   {
     StageTimer timer("kernel loading");
-    CUTRITON_RETURN_IF_ERROR(PrepareKernels());
+    CUTRITON_RETURN_IF_ERROR(PrepareKernels(true));
   }
+  void* scratch = runtime_scratch_ ? runtime_scratch_->data() : nullptr;
+  const std::size_t scratch_bytes = runtime_scratch_ ? runtime_scratch_->size_bytes() : 0;
 
   const Device& device = state_->plan.backend_options().device;
   if (device.type != DeviceType::kHIP) {
@@ -979,8 +881,8 @@ Status ExecutionContext::RunAsync(void* stream) {
     for (std::size_t i = 0; i < kernels_.size(); ++i) {
       const PlanOp& op = state_->plan.ops()[i];
       const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
-      KernelContext context{&node, &tensors_, stream,
-                            state_->plan.enable_profiling() ? &profiler_ : nullptr, ScratchPointer(), ScratchBytes()};
+      KernelContext context{&node, &tensors_, stream, state_->plan.enable_profiling() ? &profiler_ : nullptr,
+                            scratch, scratch_bytes};
       for (auto& kernel : kernels_[i]) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
     }
     run_pending_ = true;
@@ -996,14 +898,13 @@ Status ExecutionContext::RunAsync(void* stream) {
   hip->active_stream = stream == nullptr ? hip->owned_stream : stream;
 
   if (!state_->plan.enable_cuda_graph()) {
-    CUTRITON_RETURN_IF_ERROR(EnqueueOps(hip->active_stream, false));
+    CUTRITON_RETURN_IF_ERROR(EnqueueOps(hip->active_stream, false, scratch, scratch_bytes));
     run_pending_ = true;
     return Status::OK();
   }
 
   std::ostringstream key;
-  key << "profile:" << selected_profile_ << "|workspace:"
-      << (workspace_ == nullptr ? nullptr : workspace_->data());
+  key << "profile:" << selected_profile_ << "|workspace:" << (workspace_ == nullptr ? nullptr : workspace_->data());
   for (const auto& name : ActiveGraph().inputs()) {
     const Tensor& t = tensors_.at(name);
     key << "|in:" << name << ':' << t.buffer()->data() << ':' << t.byte_offset();
@@ -1017,8 +918,7 @@ Status ExecutionContext::RunAsync(void* stream) {
     key << "|candidate:" << state_->plan.ops()[i].candidates[selected_candidates_[i]].candidate_id;
   }
   const std::string graph_key = key.str();
-  auto entry = std::find_if(hip->graphs.begin(), hip->graphs.end(),
-                            [&](const GraphEntry& e) { return e.key == graph_key; });
+  auto entry = std::find_if(hip->graphs.begin(), hip->graphs.end(), [&](const GraphEntry& e) { return e.key == graph_key; });
   if (entry == hip->graphs.end()) {
     GraphEntry created;
     created.key = graph_key;
@@ -1052,7 +952,8 @@ Status ExecutionContext::TimeOp(std::size_t op_index, int iterations, void* stre
   // Flatten is a view: no launch, not timed (as in the profiled graph).
   if (kernels_[op_index].empty() || node.op_type() == "Flatten") return Status::OK();
   void* s = stream == nullptr ? hip->owned_stream : stream;
-  KernelContext context{&node, &tensors_, s, nullptr, ScratchPointer(), ScratchBytes()};
+  KernelContext context{&node, &tensors_, s, nullptr, runtime_scratch_ ? runtime_scratch_->data() : nullptr,
+                        runtime_scratch_ ? runtime_scratch_->size_bytes() : 0};
   cth_event start = nullptr;
   cth_event end = nullptr;
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_set_device(state_->plan.backend_options().device.id), "hipSetDevice"));
@@ -1080,21 +981,18 @@ Status ExecutionContext::TimeOp(std::size_t op_index, int iterations, void* stre
 
 Status ExecutionContext::Synchronize() {
   if (!run_pending_) return Status::OK();
-  if (state_->plan.backend_options().device.type != DeviceType::kHIP) {
-    run_pending_ = false;
-    return Status::OK();
-  }
-  auto* hip = static_cast<HipExecutionState*>(hip_state_);
   run_pending_ = false;
-  CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(hip->active_stream), "hipStreamSynchronize"));
+  if (state_->plan.backend_options().device.type != DeviceType::kHIP) return Status::OK();
   profiler_.Clear();
+  auto* hip = static_cast<HipExecutionState*>(hip_state_);
+  CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(hip->active_stream), "hipStreamSynchronize"));
   if (state_->plan.enable_profiling()) {
     for (std::size_t i = 0; i < state_->plan.ops().size(); ++i) {
       const PlanOp& op = state_->plan.ops()[i];
       float ms = 0.0f;
       if (hip->events[i].timed) {
-        CUTRITON_RETURN_IF_ERROR(RuntimeStatus(
-            cth_event_elapsed_ms(&ms, hip->events[i].start, hip->events[i].end), "hipEventElapsedTime"));
+        CUTRITON_RETURN_IF_ERROR(
+            RuntimeStatus(cth_event_elapsed_ms(&ms, hip->events[i].start, hip->events[i].end), "hipEventElapsedTime"));
       }
       profiler_.Record(op.node_name, op.backend_name, static_cast<double>(ms));
     }

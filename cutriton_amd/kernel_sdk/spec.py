@@ -55,7 +55,14 @@ CONSTRAINTS: dict[str, frozenset[str]] = {
     "tensor_rank_eq": frozenset({"kind", "source", "index", "value"}),
     # shape[axis] of an input/output is at most value
     "dim_le": frozenset({"kind", "source", "index", "axis", "value"}),
+    # every input and output tensor bound by the kernel holds at most value bytes
+    "tensor_bytes_le": frozenset({"kind", "value"}),
 }
+
+# Constraint of every kernel that addresses its tensors through 32-bit buffer
+# resources (__builtin_amdgcn_make_buffer_rsrc with a byte count of type int):
+# no tensor it binds may reach 2 GiB.
+BUFFER_RESOURCE_LIMIT: dict[str, Any] = {"kind": "tensor_bytes_le", "value": 2**31 - 1}
 
 ARGUMENT_TYPES = frozenset({"*fp32", "*fp16", "*i8", "i32", "fp32"})
 
@@ -145,6 +152,8 @@ class KernelSpec:
                 raise ValueError(f"{self.kernel_id}: invalid tensor constraint source")
             if kind == "dim_le" and (not isinstance(constraint.get("axis"), int) or constraint["axis"] < 0):
                 raise ValueError(f"{self.kernel_id}: dim_le needs a non-negative axis")
+            if kind == "tensor_bytes_le" and (not isinstance(constraint.get("value"), int) or constraint["value"] <= 0):
+                raise ValueError(f"{self.kernel_id}: tensor_bytes_le needs a positive byte count")
 
 
 def _validate_grid(kernel_id: str, grid: Any, variants: tuple[KernelVariant, ...]) -> None:

@@ -11,6 +11,7 @@ kernel: they take the reference convolution / Gemm ABI with one more input.
 from __future__ import annotations
 
 from cutriton_amd.kernel_sdk.spec import (
+    BUFFER_RESOURCE_LIMIT,
     KernelSpec,
     KernelVariant,
     arg,
@@ -152,10 +153,13 @@ def register_conv_family() -> None:
             for i, name in enumerate(("x", "weight", "scale", "bias", "mean", "variance"))
         )
     epsilon = arg("epsilon", "fp32", "attribute_f64", name="batchnorm_epsilon", default=1e-5)
-    families = ((CONV_SOURCE, "mfma", conv_variants, CONV_GRID, "OHWI", ()),
-                (CONV_SOURCE, "splitk", split_variants, SPLIT_GRID, "OHWI", ()),
-                (DIRECT_SOURCE, "direct", direct_variants, CONV_GRID, None, ()),
-                (SMALLC_SOURCE, "smallc", smallc_variants, SMALLC_GRID, None, SMALLC_CONSTRAINTS))
+    # Every family addresses x, the weight, the residual and y through 32-bit
+    # buffer resources.
+    limit = (BUFFER_RESOURCE_LIMIT,)
+    families = ((CONV_SOURCE, "mfma", conv_variants, CONV_GRID, "OHWI", limit),
+                (CONV_SOURCE, "splitk", split_variants, SPLIT_GRID, "OHWI", limit),
+                (DIRECT_SOURCE, "direct", direct_variants, CONV_GRID, None, limit),
+                (SMALLC_SOURCE, "smallc", smallc_variants, SMALLC_GRID, None, SMALLC_CONSTRAINTS + limit))
     residual = (arg("residual", "*fp32", "input", index=6),)
     for op_type, kernel_id, prefix, extra in (
         ("FusedConvBatchNormRelu", "conv_bn_relu.fp32.nchw", "conv_bn_relu_fp32", ()),
@@ -198,6 +202,7 @@ def register_gemm() -> None:
             {"kind": "attribute_i64_eq", "name": "transB", "value": trans_b, "default": 0},
             {"kind": "tensor_rank_eq", "source": "input", "index": 0, "value": 2},
             {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 2},
+            BUFFER_RESOURCE_LIMIT,  # the conv core's 32-bit buffer resources
         )
         dims = (
             arg("m", "i32", "input_dim", index=0, axis=0),

@@ -11,6 +11,7 @@ insert ``bias`` (input 2) after ``b``.
 from __future__ import annotations
 
 from cutriton_amd.kernel_sdk.spec import (
+    BUFFER_RESOURCE_LIMIT,
     KernelSpec,
     KernelVariant,
     arg,
@@ -115,6 +116,8 @@ def register_gemms() -> None:
             ("_tb", GEMM_NT_SOURCE, nt_variants, {}, 1),
         ):
             constraints = ({"kind": "input_count_eq", "value": len(inputs)},) + gemm_constraints(trans_b)
+            if source == GEMM_NT_SOURCE:  # 32-bit buffer resources over A and B
+                constraints += (BUFFER_RESOURCE_LIMIT,)
             if bias:
                 constraints += ({"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 1},)
             arguments = tuple(
@@ -234,6 +237,7 @@ def register_attention() -> None:
                 {"kind": "tensor_rank_eq", "source": "input", "index": 1, "value": 4},
                 {"kind": "tensor_rank_eq", "source": "input", "index": 2, "value": 4},
                 {"kind": "dim_le", "source": "input", "index": 0, "axis": 3, "value": dmax},
+                BUFFER_RESOURCE_LIMIT,  # K is read through a 32-bit buffer resource
             ),
         ))
 

@@ -40,6 +40,23 @@ def _compile(source: Path) -> Path:
     return obj
 
 
+# HIP sources compiled for host and gfx950 into the library itself (their
+# device symbols are registered with the HIP runtime when it loads).
+LIBRARY_HIP_SOURCES: tuple[str, ...] = ()
+
+
+def _compile_library_hip(relative: str) -> Path:
+    from .kernel_sdk.builder import HIPCC_FLAGS, hipcc
+
+    source = CSRC_DIR / relative
+    obj = BUILD_DIR / (relative.replace("/", "_") + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", "-fPIC", f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", str(source), "-o", str(obj)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source}:\n{result.stderr}")
+    return obj
+
+
 def _embedded_relayout_code() -> Path:
     """Compiles ``relayout.hip`` to a gfx950 code object and compiles that
     object into the library as ``cutriton::kRelayoutCodeObject``."""
@@ -70,7 +87,8 @@ def build_engine_library(jobs: int = 8) -> Path:
     sources = sorted(CSRC_DIR.rglob("*.cc"))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         embedded = pool.submit(_embedded_relayout_code)
-        objects = list(pool.map(_compile, sources)) + [embedded.result()]
+        device_objects = [pool.submit(_compile_library_hip, relative) for relative in LIBRARY_HIP_SOURCES]
+        objects = list(pool.map(_compile, sources)) + [embedded.result()] + [f.result() for f in device_objects]
     staging = LIBRARY_PATH.with_suffix(".so.tmp")
     cmd = ["g++", "-shared", "-o", str(staging), *map(str, objects),
            f"-L{ROCM / 'lib'}", f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64"]

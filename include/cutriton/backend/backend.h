@@ -97,6 +97,12 @@ std::shared_ptr<Backend> CreateCpuReferenceBackend();
 std::shared_ptr<Backend> CreateHipBackend();
 Status RegisterBuiltinBackends();
 
+// Checks the size-dependent constraints (tensor_bytes_le) of every kernel
+// step of `candidate` against the value shapes of `graph` (a graph resolved at
+// some shape-profile point). Candidate temporaries are sized like their
+// "like" value. Unsupported names the first tensor that is too large.
+Status CheckCandidateShapes(const ExecutionCandidate& candidate, const Graph& graph);
+
 // Numeric architecture of a HIP device (950 for gfx950), used against
 // min_compute_capability; `arch_name` receives e.g. "gfx950".
 Status DeviceArchitecture(int device_id, int* numeric_arch, std::string* arch_name);
@@ -107,5 +113,8 @@ Status CreateInvocationKernel(const KernelInvocation& invocation, int device_id,
                               std::shared_ptr<HipModuleCache> cache,
                               std::unique_ptr<OpKernel>* kernel);
 std::size_t LoadedModuleCount(const std::shared_ptr<HipModuleCache>& cache);
+// Whether the code object of `artifact` is loaded (CreateInvocationKernel
+// then loads nothing).
+bool CodeObjectLoaded(const std::shared_ptr<HipModuleCache>& cache, const KernelArtifact& artifact);
 
 }  // namespace cutriton

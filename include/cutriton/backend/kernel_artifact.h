@@ -75,6 +75,10 @@ enum class KernelConstraintKind {
   kInputCountEquals,
   kTensorRankEquals,
   kTensorDimAtMost,  // "dim_le": shape[axis] of an input/output <= value
+  // "tensor_bytes_le": every input and output the kernel binds holds at most
+  // value bytes (kernels that address tensors through 32-bit buffer
+  // resources declare 2^31 - 1).
+  kTensorBytesAtMost,
 };
 
 // Declarative constraint; packs cannot inject code.

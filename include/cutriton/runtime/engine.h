@@ -63,15 +63,21 @@ class ExecutionContext {
   Status TimeOp(std::size_t op_index, int iterations, void* stream, double* ms_per_launch);
 
  private:
-  Status PrepareKernels();
-  Status PrepareTuning();
-  Status PrepareTensors();
+  // What a binding or shape change invalidates, from least to most.
+  enum class Stale { kBindings, kShapes, kProfile };
+  void Invalidate(Stale what);
+  // With a "may_*" flag false, a step that would allocate device memory,
+  // load a code object or time candidates fails instead.
+  Status PrepareKernels(bool may_load);
+  Status PrepareTuning(bool may_time);
+  Status PrepareTensors(bool may_allocate);
   Status ValidateBindings() const;
-  Status EnqueueOps(void* stream, bool capture);
+  Status EnqueueOps(void* stream, bool capture, void* scratch, std::size_t scratch_bytes);
   Status CaptureGraph(void* stream, void** exec);
   void InvalidateHipGraph();
   const Graph& ActiveGraph() const;
   const MemoryPlan& ActiveMemoryPlan() const;
+  std::size_t RuntimeScratchNeed() const;
 
   std::shared_ptr<EngineState> state_;
   bool kernels_prepared_{false};
@@ -85,11 +91,11 @@ class ExecutionContext {
   bool shapes_resolved_{false};
   std::vector<std::vector<std::unique_ptr<OpKernel>>> kernels_;
   std::unordered_map<std::string, Tensor> tensors_;
+  // Caller-bound graph inputs and outputs (the rest of tensors_ is derived).
+  std::unordered_map<std::string, Tensor> bound_;
   std::shared_ptr<Buffer> workspace_;
   // Zero-initialised device scratch for kernels that declare one.
   std::shared_ptr<Buffer> runtime_scratch_;
-  void* ScratchPointer() const { return runtime_scratch_ ? runtime_scratch_->data() : nullptr; }
-  std::size_t ScratchBytes() const { return runtime_scratch_ ? runtime_scratch_->size_bytes() : 0; }
   Profiler profiler_;
   // HIP stream/event/graph state; its type lives in the implementation.
   void* hip_state_{nullptr};

@@ -205,3 +205,43 @@ def test_wrong_architecture_pack_is_unsupported(monkeypatch):
     with pytest.raises(engine.CutritonError) as err:
         engine.build_engine(workloads.to_model(workloads.conv_bn_relu()[0]), engine.CompileOptions())
     assert err.value.kind == "Unsupported"
+
+
+def test_buffer_resource_kernels_refuse_two_gibibyte_tensors(gfx950):
+    """Kernels that address tensors through 32-bit buffer resources declare
+    tensor_bytes_le 2^31 - 1. A ResNet-50 profile whose max batch (1024)
+    makes the stem's output 3.3 GB leaves the stem convolution without a
+    kernel at that corner: the build fails and names the tensor, instead of
+    planning a run whose padded reads would wrap (the reference's i32
+    narrowing checks play this part, src/backend/cuda_launcher.cpp:140-192)."""
+    graph = workloads.resnet50(1)
+    opts = engine.CompileOptions(shape_profiles={"batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224),
+                                                                     (1024, 3, 224, 224))}})
+    with pytest.raises(engine.CutritonError) as refused:
+        engine.build_engine(workloads.to_model(graph), opts)
+    assert refused.value.kind == "Unsupported", refused.value
+    assert "2147483647" in str(refused.value) and "stem" in str(refused.value)
+    # The same profile up to batch 64 plans (every tensor stays below 2 GiB).
+    ok = engine.CompileOptions(shape_profiles={"batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224),
+                                                                   (64, 3, 224, 224))}})
+    assert len(engine.build_engine(workloads.to_model(graph), ok).ops()) == 57
+    # A static graph of batch 1024 is refused at lowering already.
+    with pytest.raises(engine.CutritonError) as static:
+        engine.build_engine(workloads.to_model(workloads.resnet50(1024)), engine.CompileOptions())
+    assert static.value.kind == "Unsupported"
+
+
+def test_tensor_bytes_constraint_is_declared_by_every_buffer_resource_kernel():
+    """Every pack entry whose source builds 32-bit buffer resources carries
+    the byte limit."""
+    import json
+
+    from cutriton_amd.kernel_sdk.builder import KERNEL_SOURCE_DIR
+
+    manifest = json.loads((native.PACK_DIR / "pack.json").read_text())
+    uses_resources = {p.stem for p in KERNEL_SOURCE_DIR.glob("*.hip") if "make_buffer_rsrc" in p.read_text()}
+    assert uses_resources >= {"conv_fp32", "gemm_fp16_nt", "attention_fp16"}
+    for entry in manifest["kernels"]:
+        if Path(entry["binary"]).stem in uses_resources:
+            limits = [c for c in entry["constraints"] if c["kind"] == "tensor_bytes_le"]
+            assert limits == [{"kind": "tensor_bytes_le", "value": 2**31 - 1}], entry["kernel_id"]

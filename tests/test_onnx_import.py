@@ -78,8 +78,10 @@ def test_hand_assembled_model_matches_the_schema_encoder(gfx950):
 
 # ---- files written by libtorch --------------------------------------------------
 
-FUSED_CNN_PLAN = ["FusedConvBatchNormRelu", "MaxPool", "FusedConvBatchNormRelu", "FusedConvBatchNorm",
-                  "FusedConvBatchNormRelu", "FusedConvBatchNormAddRelu", "GlobalAveragePool", "Flatten", "Gemm"]
+# Nodes keep the exporter's order where dependencies allow; the shortcut
+# convolution comes last in the block, so it takes the residual join.
+FUSED_CNN_PLAN = ["FusedConvBatchNormRelu", "MaxPool", "FusedConvBatchNormRelu", "FusedConvBatchNormRelu",
+                  "FusedConvBatchNorm", "FusedConvBatchNormAddRelu", "GlobalAveragePool", "Flatten", "Gemm"]
 
 
 @pytest.mark.parametrize("name", CNN_FIXTURES)
