@@ -397,6 +397,11 @@ int ct_context_run_async(ct_context* context, void* stream) {
   return Report(context->context->RunAsync(stream));
 }
 
+int ct_context_run_async_no_alloc(ct_context* context, void* stream) {
+  if (context == nullptr) return Invalid("context is null");
+  return Report(context->context->RunAsyncWithoutAllocation(stream));
+}
+
 int ct_context_synchronize(ct_context* context) {
   if (context == nullptr) return Invalid("context is null");
   return Report(context->context->Synchronize());

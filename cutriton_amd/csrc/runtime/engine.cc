@@ -40,6 +40,7 @@
 #include "cutriton/ir/pass.h"
 #include "cutriton_hip_runtime.h"
 #include "runtime/relayout.h"
+#include "runtime/static_scratch.h"
 #include "runtime/tuning_store.h"
 
 namespace cutriton {
@@ -940,6 +941,49 @@ Status ExecutionContext::RunAsync(void* stream) {
   return Status::OK();
 }
 
+// The allocation-free run: the same preparation with every allocating step
+// refused, then the ops enqueued straight onto the caller's stream with the
+// static scratch as their runtime scratch.
+Status ExecutionContext::RunAsyncWithoutAllocation(void* stream) {
+  if (run_pending_) return Status::RuntimeError("a run is already pending");
+  if (stream == nullptr) return Status::InvalidArgument("the allocation-free run needs the caller's stream");
+  if (state_ == nullptr) return Status::InvalidArgument("ExecutionContext has no EngineState");
+  const Device& device = state_->plan.backend_options().device;
+  if (device.type != DeviceType::kHIP) return Status::Unsupported("the allocation-free run needs a HIP plan");
+  const std::size_t need = RuntimeScratchNeed();
+  if (need > kStaticScratchBytes) {
+    return Status::InvalidArgument("kernels of this plan declare " + std::to_string(need) +
+                                     " bytes of runtime scratch; the static scratch holds " +
+                                     std::to_string(kStaticScratchBytes));
+  }
+  CUTRITON_RETURN_IF_ERROR(PrepareTensors(false));
+  CUTRITON_RETURN_IF_ERROR(ValidateBindings());
+  CUTRITON_RETURN_IF_ERROR(PrepareTuning(false));
+  CUTRITON_RETURN_IF_ERROR(PrepareKernels(false));
+  void* scratch = nullptr;
+  if (StaticScratchAddress(device.id, &scratch) != 0) {
+    return Status::RuntimeError(std::string("static scratch: ") + StaticScratchError());
+  }
+  CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_set_device(device.id), "hipSetDevice"));
+  // The array keeps the last call's contents: the split-K tile counters must
+  // start at zero.
+  if (need > 0 && ClearStaticScratchCounters(scratch, stream) != 0) {
+    return Status::RuntimeError(std::string("static scratch: ") + StaticScratchError());
+  }
+  if (auto* hip = static_cast<HipExecutionState*>(hip_state_)) {
+    for (auto& pair : hip->events) pair.timed = false;  // no per-op events on this path
+  }
+  for (std::size_t i = 0; i < kernels_.size(); ++i) {
+    const PlanOp& op = state_->plan.ops()[i];
+    const Node& node = ActiveGraph().nodes().at(static_cast<std::size_t>(op.node_id));
+    KernelContext context{&node, &tensors_, stream, nullptr, scratch, kStaticScratchBytes};
+    for (auto& kernel : kernels_[i]) CUTRITON_RETURN_IF_ERROR(kernel->Compute(&context));
+  }
+  unmanaged_stream_ = stream;
+  run_pending_ = true;
+  return Status::OK();
+}
+
 Status ExecutionContext::TimeOp(std::size_t op_index, int iterations, void* stream, double* ms_per_launch) {
   if (ms_per_launch == nullptr || iterations < 1) return Status::InvalidArgument("TimeOp needs iterations >= 1");
   if (run_pending_) return Status::RuntimeError("TimeOp while a run is pending");
@@ -984,6 +1028,11 @@ Status ExecutionContext::Synchronize() {
   run_pending_ = false;
   if (state_->plan.backend_options().device.type != DeviceType::kHIP) return Status::OK();
   profiler_.Clear();
+  if (unmanaged_stream_ != nullptr) {  // an allocation-free run: no events were recorded
+    void* stream = unmanaged_stream_;
+    unmanaged_stream_ = nullptr;
+    return RuntimeStatus(cth_stream_synchronize(stream), "hipStreamSynchronize");
+  }
   auto* hip = static_cast<HipExecutionState*>(hip_state_);
   CUTRITON_RETURN_IF_ERROR(RuntimeStatus(cth_stream_synchronize(hip->active_stream), "hipStreamSynchronize"));
   if (state_->plan.enable_profiling()) {

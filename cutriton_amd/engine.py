@@ -93,6 +93,7 @@ def _lib() -> ctypes.CDLL:
         "ct_context_resolved_desc": (I, [P, C, c_int64_p, ctypes.POINTER(I), ctypes.POINTER(I), C, S]),
         "ct_context_run": (I, [P]),
         "ct_context_run_async": (I, [P, P]),
+        "ct_context_run_async_no_alloc": (I, [P, P]),
         "ct_context_synchronize": (I, [P]),
         "ct_context_profile_event_count": (I, [P]),
         "ct_context_profile_event": (I, [P, I, C, S, ctypes.POINTER(D)]),
@@ -394,6 +395,11 @@ class ExecutionContext:
 
     def run_async(self, stream: int | None = None) -> None:
         _check(self._lib.ct_context_run_async(self.handle, ctypes.c_void_p(stream or 0)))
+
+    def run_async_no_alloc(self, stream: int) -> None:
+        """ct_context_run_async_no_alloc: the run that allocates no device
+        memory (the kernels' scratch is the library's static array)."""
+        _check(self._lib.ct_context_run_async_no_alloc(self.handle, ctypes.c_void_p(stream)))
 
     def synchronize(self) -> None:
         _check(self._lib.ct_context_synchronize(self.handle))

@@ -42,7 +42,7 @@ def _compile(source: Path) -> Path:
 
 # HIP sources compiled for host and gfx950 into the library itself (their
 # device symbols are registered with the HIP runtime when it loads).
-LIBRARY_HIP_SOURCES: tuple[str, ...] = ()
+LIBRARY_HIP_SOURCES = ("runtime/static_scratch.hip",)
 
 
 def _compile_library_hip(relative: str) -> Path:

@@ -47,6 +47,18 @@ class ExecutionContext {
   Status Run();
   // Enqueues on `stream` (a hipStream_t), or on the context's own stream.
   Status RunAsync(void* stream);
+  // RunAsync for callers that cannot allocate device memory (no counterpart
+  // in the reference). It enqueues the op sequence on `stream` (non-null)
+  // without graph capture and without per-op events, binding the kernels'
+  // runtime scratch to the library's static device array; it calls no
+  // hipMalloc, loads no code object and times no candidate. What it needs
+  // must already exist: constants uploaded, a workspace of the profile's
+  // size, the code objects of the selected kernels loaded (one RunAsync of
+  // the context, at any shape of its profile, provides all three) and
+  // tuning choices that resolve without timing. Otherwise it fails with
+  // RuntimeError and enqueues nothing. Runs of this kind that overlap on one
+  // GPU share the static array and race.
+  Status RunAsyncWithoutAllocation(void* stream);
   Status Synchronize();
 
   const Profiler& profiler() const { return profiler_; }
@@ -66,8 +78,9 @@ class ExecutionContext {
   // What a binding or shape change invalidates, from least to most.
   enum class Stale { kBindings, kShapes, kProfile };
   void Invalidate(Stale what);
-  // With a "may_*" flag false, a step that would allocate device memory,
-  // load a code object or time candidates fails instead.
+  // The "may_*" flags are false on the allocation-free path: a step that
+  // would allocate device memory, load a code object or time candidates
+  // fails instead.
   Status PrepareKernels(bool may_load);
   Status PrepareTuning(bool may_time);
   Status PrepareTensors(bool may_allocate);
@@ -99,6 +112,8 @@ class ExecutionContext {
   Profiler profiler_;
   // HIP stream/event/graph state; its type lives in the implementation.
   void* hip_state_{nullptr};
+  // Stream of a pending allocation-free run (Synchronize waits on it).
+  void* unmanaged_stream_{nullptr};
 };
 
 }  // namespace cutriton

@@ -130,6 +130,21 @@ int ct_context_resolved_desc(const ct_context* context, const char* name, int64_
                              int* rank, int* dtype, char* layout, size_t layout_length);
 int ct_context_run(ct_context* context);
 int ct_context_run_async(ct_context* context, void* stream);
+/* Allocation-free variant of ct_context_run_async, for callers that cannot
+ * allocate device memory: code under stream capture, serving loops that
+ * forbid hipMalloc. No counterpart in the reference. It enqueues the op
+ * sequence on `stream` (required) with no graph capture and no per-op events,
+ * binding the kernels' runtime scratch (split-K partial sums and tile
+ * counters) to the library's static device array of 64 KiB + 128 MiB, held by
+ * every GPU the library runs on until the process ends; it calls no
+ * hipMalloc/hipFree, loads no code object and times no candidate. The context
+ * must already hold its constants, a workspace for its profile and the code
+ * objects of its kernels (one ct_context_run_async of the context at any shape
+ * of its profile provides them), and its tuning choices must resolve without
+ * timing; otherwise it returns an error and enqueues nothing. Calls that
+ * overlap on one GPU share the array and race. Complete with
+ * ct_context_synchronize. Forwards to ExecutionContext::RunAsyncWithoutAllocation. */
+int ct_context_run_async_no_alloc(ct_context* context, void* stream);
 int ct_context_synchronize(ct_context* context);
 int ct_context_profile_event_count(const ct_context* context);
 int ct_context_profile_event(const ct_context* context, int index, char* name,
