@@ -72,6 +72,8 @@ GEMM_NT_TILES = (
     ("m128n128w8", 128, 128, 64, 8),
     ("m128n128k128w8", 128, 128, 128, 8),
     ("m128n64w8", 128, 64, 64, 8),
+    # 2 x 2 wavefront tiles times 2 depth groups that split each 128-deep stage
+    ("m128n128k128w2x2k2", 128, 128, 128, 8),
 )
 GEMM_NT_DEFAULT = "m128n128w4"
 

@@ -125,19 +125,28 @@ struct NtShape {
 // VEC: k is a multiple of 8, so every 16-byte chunk is 8 depths of one row
 // and the tiles load straight into LDS; otherwise chunks are assembled
 // element by element through registers.
-template <int BM, int BN, int BK, int STAGES, int WAVES_M, int WAVES_N, bool GELU, bool BIAS, bool VEC>
+//
+// WAVES_K > 1 splits each depth tile among WAVES_K groups of WAVES_M x
+// WAVES_N wavefronts: group g multiplies steps [g, g + 1) * STEPS / WAVES_K
+// of every stage for the whole output tile, so each wavefront's tile is
+// WAVES_K times larger (fewer LDS fragment reads per MFMA), and the groups'
+// partial sums are added through the idle LDS ring after the last stage.
+template <int BM, int BN, int BK, int STAGES, int WAVES_M, int WAVES_N, bool GELU, bool BIAS, bool VEC, int WAVES_K = 1>
 __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float16* __restrict__ a,
                                            const _Float16* __restrict__ bt, const _Float16* __restrict__ bias,
                                            _Float16* __restrict__ output, const int m, const int n, const int k) {
   using S = NtShape<BM, BN, BK, STAGES>;
   constexpr int CH = S::kChunks;
   constexpr int RPL = S::kRowsPerLoad;
-  constexpr int WAVES = WAVES_M * WAVES_N;
+  constexpr int TILE_WAVES = WAVES_M * WAVES_N;
+  constexpr int WAVES = TILE_WAVES * WAVES_K;
   constexpr int WM = BM / WAVES_M;
   constexpr int WN = BN / WAVES_N;
   constexpr int TM = WM / 16;
   constexpr int TN = WN / 16;
   constexpr int STEPS = BK / 32;
+  constexpr int GROUP_STEPS = STEPS / WAVES_K;  // MFMA steps per stage and wavefront
+  static_assert(GROUP_STEPS * WAVES_K == STEPS, "the depth groups split a stage's steps evenly");
   constexpr int LOADS = (BM + BN) / RPL / WAVES;  // load instructions per wavefront and tile
   static_assert(BK == 64 || BK == 128, "depth tile of 2 or 4 MFMA steps");
   static_assert(STAGES >= 2 && STAGES <= 4, "ring of 2..4 stages");
@@ -201,8 +210,10 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[t][i][r] = 0.0f;
 
-  const int wm = (wave / WAVES_N) * WM;
-  const int wn = (wave % WAVES_N) * WN;
+  const int wk = wave / TILE_WAVES;  // depth group
+  const int wmn = wave % TILE_WAVES;
+  const int wm = (wmn / WAVES_N) * WM;
+  const int wn = (wmn % WAVES_N) * WN;
   const int lane16 = lane & 15;
   const int quarter = lane >> 4;
   // Fragment rows are lane16 plus a multiple of 16, so f(row) = f(lane16).
@@ -217,10 +228,11 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   // pipeline instead of stalling it.
   auto compute_tile = [&](int stage) {
     const u32x4* tile_base = lds + stage * S::kStageChunks;
+    const int first_step = wk * GROUP_STEPS;
     f16x8 af[2][TM];
     f16x8 bf[2][TN];
     auto read_frags = [&](int step, f16x8* fa, f16x8* fb) {
-      const int chunk = (4 * step + quarter) ^ swz;
+      const int chunk = (4 * (first_step + step) + quarter) ^ swz;
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i] = __builtin_bit_cast(f16x8, tile_base[a_row + i * 16 * CH + chunk]);
 #pragma unroll
@@ -228,9 +240,9 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     };
     read_frags(0, af[0], bf[0]);
 #pragma unroll
-    for (int step = 0; step < STEPS; ++step) {
+    for (int step = 0; step < GROUP_STEPS; ++step) {
       const int cur_f = step & 1;
-      if (step + 1 < STEPS) read_frags(step + 1, af[cur_f ^ 1], bf[cur_f ^ 1]);
+      if (step + 1 < GROUP_STEPS) read_frags(step + 1, af[cur_f ^ 1], bf[cur_f ^ 1]);
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
@@ -242,8 +254,8 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS, 0);
 #pragma unroll
-    for (int step = 0; step < STEPS; ++step) {
-      if (step + 1 < STEPS) {
+    for (int step = 0; step < GROUP_STEPS; ++step) {
+      if (step + 1 < GROUP_STEPS) {
 #pragma unroll
         for (int q = 0; q < PAIRS; ++q) {
           __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
@@ -283,6 +295,36 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     compute_tile(kt % STAGES);
   }
 
+  // Depth groups: group 0 adds the partial sums of groups 1..WAVES_K-1,
+  // one group at a time through the idle LDS ring ([wmn][register][lane]
+  // floats, one wavefront's accumulators per 64-lane row).
+  if constexpr (WAVES_K > 1) {
+    constexpr int REGS = TM * TN * 4;
+    static_assert(TILE_WAVES * REGS * 64 * 4 <= S::kLdsChunks * 16, "one group's partial sums fit the LDS ring");
+    float* partial = reinterpret_cast<float*>(lds) + wmn * REGS * 64 + lane;
+#pragma unroll 1
+    for (int g = 1; g < WAVES_K; ++g) {
+      __syncthreads();  // the ring (or the previous group's sums) is free
+      if (wk == g) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) partial[((t * TM + i) * 4 + r) * 64] = acc[t][i][r];
+      }
+      __syncthreads();
+      if (wk == 0) {
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][i][r] += partial[((t * TM + i) * 4 + r) * 64];
+      }
+    }
+  }
+
   // Epilogue: lane holds row m = m0 + wm + 16 i + lane16 and columns
   // n = n0 + wn + 16 t + 4 quarter + 0..3.
   if ((n & 7) == 0) {
@@ -304,29 +346,31 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     constexpr int THREADS = 64 * WAVES;
     static_assert(BM * BN * 2 <= S::kLdsChunks * 16, "output tile fits the LDS ring");
     static_assert((BM * CHN) % THREADS == 0, "whole rounds of chunk stores");
-    __syncthreads();  // every wavefront is done reading the last depth tile
+    __syncthreads();  // every wavefront is done reading the last depth tile (or partial sums)
     _Float16* tile_h = reinterpret_cast<_Float16*>(lds);
+    if (wk == 0) {  // depth groups 1.. handed their sums to group 0
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int lc = wn + t * 16 + 4 * quarter;
-      float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (BIAS) {
+      for (int t = 0; t < TN; ++t) {
+        const int lc = wn + t * 16 + 4 * quarter;
+        float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (BIAS) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bias4[e] = n0 + lc + e < n ? static_cast<float>(bias[n0 + lc + e]) : 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int lr = wm + i * 16 + lane16;
-        f16x4 out4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = acc[t][i][e];
-          if (BIAS) v += bias4[e];
-          if (GELU) v = GeluErfAs(v);
-          out4[e] = static_cast<_Float16>(v);
+          for (int e = 0; e < 4; ++e) bias4[e] = n0 + lc + e < n ? static_cast<float>(bias[n0 + lc + e]) : 0.0f;
         }
-        const int pc = (lc >> 3) ^ ((lr / RSW) % SWM);
-        *reinterpret_cast<f16x4*>(tile_h + lr * BN + pc * 8 + (lc & 7)) = out4;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int lr = wm + i * 16 + lane16;
+          f16x4 out4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = acc[t][i][e];
+            if (BIAS) v += bias4[e];
+            if (GELU) v = GeluErfAs(v);
+            out4[e] = static_cast<_Float16>(v);
+          }
+          const int pc = (lc >> 3) ^ ((lr / RSW) % SWM);
+          *reinterpret_cast<f16x4*>(tile_h + lr * BN + pc * 8 + (lc & 7)) = out4;
+        }
       }
     }
     __syncthreads();
@@ -343,6 +387,7 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     return;
   }
   const bool vec_out = (n & 3) == 0;
+  if (wk != 0) return;  // depth groups 1.. handed their sums to group 0
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int col = n0 + wn + t * 16 + 4 * quarter;
@@ -379,35 +424,37 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
 }  // namespace
 
 // Entry point body: one LDS allocation shared by the two loader paths.
-#define CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, GELU, BIAS, BIAS_PTR)                                  \
-  __shared__ u32x4 lds[NtShape<BM, BN, BK, ST>::kLdsChunks];                                           \
-  if ((k & 7) == 0) {                                                                                  \
-    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, true>(lds, a, bt, BIAS_PTR, output, m, n, k);       \
-  } else {                                                                                             \
-    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, false>(lds, a, bt, BIAS_PTR, output, m, n, k);      \
+#define CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, GELU, BIAS, BIAS_PTR)                                     \
+  __shared__ u32x4 lds[NtShape<BM, BN, BK, ST>::kLdsChunks];                                                  \
+  if ((k & 7) == 0) {                                                                                         \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, true, WK>(lds, a, bt, BIAS_PTR, output, m, n, k);          \
+  } else {                                                                                                    \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, false, WK>(lds, a, bt, BIAS_PTR, output, m, n, k);         \
   }
 
-#define CT_DEFINE_GEMM_NT(NAME, BM, BN, BK, ST, WM, WN)                                                     \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
-      gemm_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,     \
-                          void*, void*) {                                                                   \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, false, false, nullptr)                                          \
-  }                                                                                                         \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
-      gemm_gelu_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k, \
-                               void*, void*) {                                                              \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, true, false, nullptr)                                           \
-  }                                                                                                         \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
-      gemm_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,                 \
-                               _Float16* output, int m, int n, int k, void*, void*) {                       \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, false, true, bias)                                              \
-  }                                                                                                         \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN)                                                            \
-      gemm_gelu_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,            \
-                                    _Float16* output, int m, int n, int k, void*, void*) {                  \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, true, true, bias)                                               \
+#define CT_DEFINE_GEMM_NT_GROUPS(NAME, BM, BN, BK, ST, WM, WN, WK)                                            \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
+      gemm_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,       \
+                          void*, void*) {                                                                     \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, false, false, nullptr)                                        \
+  }                                                                                                           \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
+      gemm_gelu_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,  \
+                               void*, void*) {                                                                \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, true, false, nullptr)                                         \
+  }                                                                                                           \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
+      gemm_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,                   \
+                               _Float16* output, int m, int n, int k, void*, void*) {                         \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, false, true, bias)                                            \
+  }                                                                                                           \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
+      gemm_gelu_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,              \
+                                    _Float16* output, int m, int n, int k, void*, void*) {                    \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, true, true, bias)                                             \
   }
+
+#define CT_DEFINE_GEMM_NT(NAME, BM, BN, BK, ST, WM, WN) CT_DEFINE_GEMM_NT_GROUPS(NAME, BM, BN, BK, ST, WM, WN, 1)
 
 // name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N
 CT_DEFINE_GEMM_NT(m256n256w4, 256, 256, 64, 2, 2, 2)
@@ -423,3 +470,5 @@ CT_DEFINE_GEMM_NT(m128n256w8, 128, 256, 64, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n128w8, 128, 128, 64, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n128k128w8, 128, 128, 128, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n64w8, 128, 64, 64, 2, 4, 2)
+// name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N, depth groups
+CT_DEFINE_GEMM_NT_GROUPS(m128n128k128w2x2k2, 128, 128, 128, 2, 2, 2, 2)

@@ -108,8 +108,8 @@ def test_ffn_plan_and_candidates(gfx950):
     assert [op.op_type for op in ops] == ["GemmGelu", "Gemm", "SkipLayerNormalization"]
     for op in ops:
         assert sum(c.startswith("unfused:") for c in op.candidates) == (0 if op.op_type == "Gemm" else 1)
-    # thirteen weight-transposed tiles, four B-as-is tiles, then Gemm,Gelu
-    assert len(ops[0].candidates) == 18
+    # fourteen weight-transposed tiles, four B-as-is tiles, then Gemm,Gelu
+    assert len(ops[0].candidates) == 19
     assert ops[0].candidates[ops[0].selected_candidate].endswith("gemm_gelu_bias.fp16.mfma:m128n128w4")
     assert ops[0].candidates[-1] == "unfused:gemm_gelu"
 
