@@ -1,30 +1,39 @@
 """Benchmark of the hot path on one MI355X.
 
 Workloads (synthetic seeded inputs, random-init weights of the named shapes):
-  * ResNet-50 v1.5, FP32 NCHW, batch 32: one step = one inference of the
-    batch through BuildEngine/ExecutionContext (53 fused conv nodes, MaxPool,
-    GAP, Flatten view, Gemm), replayed as one hipGraph. `value` is img/s.
-    Batch 64 (the top of the reference's dynamic-batch profile) on its own
-    engine is reported beside it.
-  * FP16 FFN block M=4096, H=1024, I=4096 (GemmGelu -> Gemm -> SkipLayerNorm):
-    reported as TFLOP/s of its two GEMMs beside the main line.
+  * ResNet-50 v1.5, FP32 NCHW, on one engine built with the dynamic batch
+    profile min1/opt32/max64 (workspace planned at the profile max, one
+    hipGraph per shape), run at batch 32 and 64: one step = one inference of
+    the batch through BuildEngine/ExecutionContext (53 fused conv nodes,
+    MaxPool, GAP, Flatten view, Gemm). `value` is img/s at batch 32.
+  * ResNet-50 at batch 1 on a static engine, and the single
+    FusedConvBatchNormRelu node x[1,64,56,56] * W[64,64,3,3].
+  * FP16 FFN block GemmGelu -> Gemm -> SkipLayerNorm at M=4096, H=1024,
+    I=4096 on the dynamic M profile min128/opt4096/max8192, and at M=512,
+    H=768, I=3072 on a static engine: TFLOP/s of the two GEMMs.
   * FP16 Softmax over attention scores [16*16*1024, 1024] and a standalone
-    FP16 LayerNorm of the same shape: reported as GB/s (HBM-bound) beside the
-    main line.
+    FP16 LayerNorm of the same shape: GB/s (HBM-bound).
   * Fused FP16 attention [8, 16, 2048, 128], full and causal: TFLOP/s.
 
 Timing: the first run tunes every op (TuneOnMiss, cache in a temporary
 directory). Then W untimed warm-up steps and K timed steps bracketed by
 torch.cuda.synchronize(), on an engine built from that cache with profiling
 off; each step is RunAsync on the measured stream + Synchronize, as in the
-reference harness (benchmarks/resnet50_native.cpp:281-291). A second set of K
-steps on a profiled engine (per-op HIP event pairs recorded inside the graph)
-gives each kernel's duration; the dominant kernel family (the FP32
-implicit-GEMM convolutions) is priced against the FP32 MFMA peak from those
-durations.
+reference harness (benchmarks/resnet50_native.cpp:281-291,
+benchmarks/transformer_ffn_native.cpp:188-218). Each op's kernels are then
+timed over back-to-back launches between HIP events on the same stream
+(ExecutionContext::TimeOp); the roofline blocks divide algorithmic FLOPs by
+those durations.
 
-The CPU baseline is the reference's CPU path (the same graph in PyTorch-CPU
-FP32, oracle/torch_cpu.py) on a bounded sample, timed on this host.
+HBM traffic: two child processes rerun the ResNet bs32 and FFN M=4096 engines
+from the tuning cache under `rocprofv3 --pmc FETCH_SIZE` and `--pmc
+WRITE_SIZE`, together with a Relu over 64 Mi floats whose known 256 MiB read
+and 256 MiB write calibrate both counters. The calibrated bytes per launch of
+the conv family and of the FFN GEMMs are the roofline blocks' `traffic`.
+
+The CPU baseline is the reference's CPU path (the same graphs in PyTorch-CPU
+FP32, oracle/torch_cpu.py), timed on this host: 3 warm-ups, then at least 10
+timed iterations, median reported.
 
 Prints one JSON line.
 """
@@ -32,11 +41,17 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import csv
+import dataclasses
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
 import tempfile
 import time
+from collections import defaultdict
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -47,13 +62,23 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 FP16_MFMA_PEAK_TFLOPS = 2516.6
 KERNEL_TIMING_LAUNCHES = 20
 CONV_OPS = ("FusedConvBatchNormRelu", "FusedConvBatchNorm", "FusedConvBatchNormAddRelu", "Conv")
+RESNET_PROFILE = {"batch": {"input": ((1, 3, 224, 224), (32, 3, 224, 224), (64, 3, 224, 224))}}
+FFN_SHAPE = (4096, 1024, 4096)
+FFN_PROFILE = {"tokens": {"x": ((128, 1024), (4096, 1024), (8192, 1024))}}
+FFN_SMALL_SHAPE = (512, 768, 3072)
+COPY_FLOATS = 64 << 20
+CPU_WARMUPS = 3
+CPU_MIN_ITERATIONS = 10
 
 
 def log(*args) -> None:
     print(*args, file=sys.stderr, flush=True)
 
 
-def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str):
+def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str, profiles=None):
+    """An engine and execution context for `graph` with `feeds` bound. With
+    `profiles` ({name: {input: (min, opt, max)}}) the engine is built for
+    that shape profile and the context runs at the feeds' shapes."""
     import numpy as np
     import torch
 
@@ -61,21 +86,30 @@ def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str):
 
     opts = engine.CompileOptions(tuning_mode=tuning_mode, tuning_cache_dir=cache_dir,
                                  enable_profiling=profiling, enable_cuda_graph=True,
-                                 tuning_warmup_iterations=3, tuning_measurement_iterations=10)
+                                 tuning_warmup_iterations=3, tuning_measurement_iterations=10,
+                                 shape_profiles=dict(profiles or {}))
     eng = engine.build_engine(workloads.to_model(graph), opts)
     ctx = eng.create_execution_context()
     inputs = {n: torch.from_numpy(np.ascontiguousarray(v)).to("cuda:0") for n, v in feeds.items()}
+    if profiles:
+        ctx.select_shape_profile(next(iter(profiles)))
+        for name, t in inputs.items():
+            ctx.set_input_shape(name, tuple(t.shape))
+        ctx.resolve_shapes()
     for name, t in inputs.items():
         ctx.bind_input(name, t, layout=graph.inputs[name][2])
     outputs = {}
     for name in graph.outputs:
-        shape, dtype = eng.value_desc(name)
+        if profiles:
+            shape, dtype, layout = ctx.resolved_desc(name)
+        else:
+            (shape, dtype), layout = eng.value_desc(name), eng.value_layout(name)
         outputs[name] = torch.empty(shape, dtype=getattr(torch, dtype), device="cuda:0")
-        ctx.bind_output(name, outputs[name], layout=eng.value_layout(name))
+        ctx.bind_output(name, outputs[name], layout=layout)
     return eng, ctx, (inputs, outputs)
 
 
-def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str):
+def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles=None):
     """Tunes `graph` (TuneOnMiss), then:
       1. a profiled engine replays `steps` steps and sums each op's HIP-event
          duration (kernel time, read from the event nodes inside the graph);
@@ -90,7 +124,7 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str):
 
     stream = torch.cuda.current_stream()
     handle = stream.cuda_stream
-    eng, ctx, keep = _context(graph, feeds, cache_dir, True, "tune_on_miss")
+    eng, ctx, keep = _context(graph, feeds, cache_dir, True, "tune_on_miss", profiles)
     t0 = time.perf_counter()
     ctx.run_async(handle)  # first run: tuning, module loads, graph capture
     ctx.synchronize()
@@ -108,7 +142,7 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str):
     selected = [op.candidates[s] for op, s in zip(ops, ctx.selected_candidates(len(ops)))]
     del ctx, eng, keep
 
-    eng, ctx, keep = _context(graph, feeds, cache_dir, False, "use_cache")
+    eng, ctx, keep = _context(graph, feeds, cache_dir, False, "use_cache", profiles)
     ctx.run_async(handle)
     ctx.synchronize()
     plain = [op.candidates[s] for op, s in zip(eng.ops(), ctx.selected_candidates(len(ops)))]
@@ -131,31 +165,53 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str):
     return ms_per_step, kernel_ms, graph_event_ms, ops, selected
 
 
-TRAFFIC_SUMMARY = ROOT / "profiles" / "resnet50_bs32_fp32_hbm_traffic.md"
+# --- algorithmic work --------------------------------------------------------
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per conv-family launch from the committed rocprofv3 PMC
-    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter
-    on a copy of known size). Counters need rocprofv3 around the process, so
-    the figure is read from that summary, not measured in this run."""
-    try:
-        for line in TRAFFIC_SUMMARY.read_text().splitlines():
-            if line.startswith("conv_family_hbm_bytes_per_launch ="):
-                return int(line.split("=", 1)[1])
-    except (OSError, ValueError):
-        pass
-    return None
-
-
-def bench_resnet(args, cache_dir: str, batch: int = 32) -> dict:
+def conv_family_bytes(graph) -> tuple[int, int]:
+    """(algorithmic HBM bytes, launches) of one step's fused conv nodes:
+    each reads its input and weights once and writes its output once (FP32),
+    and each residual join also reads its residual once."""
     from cutriton_amd import workloads
 
-    graph = workloads.resnet50(batch)
+    shapes = workloads.value_shapes(graph)
+
+    def size(name: str) -> int:
+        n = 1
+        for d in shapes[name]:
+            n *= d
+        return 4 * n
+
+    total = launches = 0
+    for node in graph.nodes:
+        if node.op_type == "Conv":
+            total += size(node.inputs[0]) + size(node.inputs[1]) + size(node.outputs[0])
+            launches += 1
+        elif node.op_type == "Add":
+            total += size(node.inputs[1])
+    return total, launches
+
+
+def ffn_gemm_bytes(m: int, h: int, i: int) -> tuple[int, int]:
+    """Algorithmic FP16 bytes of GemmGelu (X, W1, b1 in; [m, i] out) and of
+    Gemm ([m, i], W2, b2 in; [m, h] out)."""
+    return 2 * (m * h + h * i + i + m * i), 2 * (m * i + i * h + h + m * h)
+
+
+# --- workloads -----------------------------------------------------------------
+
+
+def bench_resnet(args, cache_dir: str, batch: int, profile: bool) -> dict:
+    from cutriton_amd import workloads
+
+    graph = workloads.resnet50(1 if profile else batch)
     x = workloads.resnet50_input(batch)
-    ms_per_step, kernel_ms, event_ms, ops, selected = run_workload(graph, {"input": x}, args.steps, args.warmup,
-                                                                   cache_dir)
-    flops = workloads.node_flops(graph)
+    ms_per_step, kernel_ms, event_ms, ops, selected = run_workload(
+        graph, {"input": x}, args.steps, args.warmup, cache_dir, RESNET_PROFILE if profile else None)
+    # The profile engine's graph is declared at batch 1; FLOPs and bytes
+    # are those of the batch it runs.
+    at_batch = dataclasses.replace(graph, inputs={"input": ((batch, 3, 224, 224), "float32", "NCHW")})
+    flops = workloads.node_flops(at_batch)
     conv_flops = sum(v for k, v in flops.items() if k != "classifier")
     total_flops = sum(flops.values())
     img_s = batch * 1e3 / ms_per_step
@@ -163,6 +219,9 @@ def bench_resnet(args, cache_dir: str, batch: int = 32) -> dict:
     conv_ms = sum(kernel_ms[i] for i in conv_idx)
     launches = len(conv_idx)
     achieved = conv_flops / (conv_ms * 1e-3) / 1e12
+    step_bytes, conv_nodes = conv_family_bytes(at_batch)
+    if conv_nodes != launches:
+        raise RuntimeError(f"{launches} conv launches for {conv_nodes} conv nodes")
 
     def op_flops(name: str) -> int:
         keys = [k for k in flops if name.startswith(k)]
@@ -170,25 +229,28 @@ def bench_resnet(args, cache_dir: str, batch: int = 32) -> dict:
 
     per_op = sorted(((kernel_ms[i], ops[i].node_name, selected[i].split(":", 1)[-1], op_flops(ops[i].node_name))
                      for i in range(len(ops))), reverse=True)
-    log(f"  resnet50 bs{batch}: {ms_per_step:.3f} ms/step, {img_s:.1f} img/s; kernel time per step: conv "
-        f"{conv_ms:.3f} ms, all {sum(kernel_ms):.3f} ms (profiled graph events {sum(event_ms):.3f} ms)")
+    engine_kind = "profile min1/opt32/max64" if profile else "static"
+    log(f"  resnet50 bs{batch} ({engine_kind} engine): {ms_per_step:.3f} ms/step, {img_s:.1f} img/s; kernel time "
+        f"per step: conv {conv_ms:.3f} ms, all {sum(kernel_ms):.3f} ms (profiled graph events {sum(event_ms):.3f} ms)")
     for ms, name, var, fl in per_op:
         rate = f"{fl / (ms * 1e-3) / 1e12:6.1f} TF/s" if fl and ms > 0 else " " * 11
         log(f"    {ms * 1e3:8.1f} us {rate}  {name}  [{var}]")
     return {
+        "engine": engine_kind,
         "ms_per_step": ms_per_step,
         "img_s": img_s,
         "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
         "pct_fp32_mfma_peak": 100.0 * total_flops / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "kernel_us": {name: round(ms * 1e3, 2) for ms, name, _, _ in per_op},
         "roofline": {
-            "kernel": "conv_bn[_add]_relu_fp32 implicit-GEMM family (53 launches/step)",
+            "kernel": f"conv_bn[_add]_relu_fp32 implicit-GEMM family ({launches} launches/step)",
             "bound": "mfma",
             "achieved": round(achieved, 3),
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": measured_traffic(),
-            "traffic_source": f"{TRAFFIC_SUMMARY.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
+            "traffic": None,
+            "algorithmic_bytes_per_launch": step_bytes // launches,
             "flop_per_launch": conv_flops / launches,
             "launches_per_step": launches,
             "avg_launch_us": conv_ms * 1e3 / launches,
@@ -198,16 +260,45 @@ def bench_resnet(args, cache_dir: str, batch: int = 32) -> dict:
     }
 
 
-def bench_ffn(args, cache_dir: str) -> dict:
+def bench_single_node(args, cache_dir: str) -> dict:
+    """The single FusedConvBatchNormRelu node: x[1,64,56,56], W[64,64,3,3],
+    stride 1, pad 1 (231.2 MFLOP)."""
     from cutriton_amd import workloads
 
-    m, h, i = 4096, 1024, 4096
-    graph, x = workloads.ffn(m, h, i)
+    graph, x = workloads.conv_bn_relu()
     ms_per_step, kernel_ms, _, ops, selected = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir)
+    flops = sum(workloads.node_flops(graph).values())
+    out = {
+        "workload": "conv_bn_relu_fp32_1x64x56x56_k3s1p1",
+        "ms_per_step": ms_per_step,
+        "kernel_us": kernel_ms[0] * 1e3,
+        "tflops": flops / (kernel_ms[0] * 1e-3) / 1e12,
+        "variant": selected[0].rsplit(":", 1)[1],
+    }
+    log(f"  single conv node: {out['kernel_us']:.1f} us kernel ({out['tflops']:.1f} TF), "
+        f"{ms_per_step * 1e3:.1f} us/step, {out['variant']}")
+    return out
+
+
+def bench_ffn(args, cache_dir: str, shape: tuple[int, int, int], profile: bool) -> dict:
+    from cutriton_amd import workloads
+
+    m, h, i = shape
+    if profile:
+        template, x = workloads.ffn(FFN_PROFILE["tokens"]["x"][2][0], h, i)
+        x = x[:m]
+    else:
+        template, x = workloads.ffn(m, h, i)
+    ms_per_step, kernel_ms, _, ops, selected = run_workload(template, {"x": x}, args.steps, args.warmup, cache_dir,
+                                                            FFN_PROFILE if profile else None)
     gemm_flops = 2 * m * h * i
     per_op = {op.op_type: kernel_ms[j] for j, op in enumerate(ops)}
+    gemm_ms = per_op["GemmGelu"] + per_op["Gemm"]
+    achieved = 2 * gemm_flops / (gemm_ms * 1e-3) / 1e12
+    gelu_bytes, gemm_bytes = ffn_gemm_bytes(m, h, i)
     out = {
         "workload": f"ffn_fp16_m{m}_h{h}_i{i}",
+        "engine": "profile min128/opt4096/max8192" if profile else "static",
         "ms_per_step": ms_per_step,
         "tflops_block": 2 * gemm_flops / (ms_per_step * 1e-3) / 1e12,
         "gemm_gelu_us": per_op["GemmGelu"] * 1e3,
@@ -216,13 +307,25 @@ def bench_ffn(args, cache_dir: str) -> dict:
         "gemm_gelu_tflops": gemm_flops / (per_op["GemmGelu"] * 1e-3) / 1e12,
         "gemm_tflops": gemm_flops / (per_op["Gemm"] * 1e-3) / 1e12,
         "skip_layer_norm_gbps": 3 * m * h * 2 / (per_op["SkipLayerNormalization"] * 1e-3) / 1e9,
-        "selected": selected,
+        "pct_fp16_mfma_peak_gemms": 100.0 * achieved / FP16_MFMA_PEAK_TFLOPS,
+        "roofline": {
+            "kernel": "FP16 GEMMs: GemmGelu + Gemm (2 launches/step)",
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": FP16_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / FP16_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": (gelu_bytes + gemm_bytes) // 2,
+            "flop_per_launch": gemm_flops,
+            "avg_launch_us": gemm_ms * 1e3 / 2,
+            "timing": f"ExecutionContext::TimeOp, {KERNEL_TIMING_LAUNCHES} back-to-back launches per op, HIP events",
+        },
+        "selected": [s.rsplit(":", 1)[1] for s in selected],
     }
-    out["pct_fp16_mfma_peak_gemms"] = 100.0 * (2 * gemm_flops) / ((per_op["GemmGelu"] + per_op["Gemm"]) * 1e-3) \
-        / 1e12 / FP16_MFMA_PEAK_TFLOPS
-    log(f"  ffn: {ms_per_step * 1e3:.1f} us/step; GemmGelu {out['gemm_gelu_us']:.1f} us "
-        f"({out['gemm_gelu_tflops']:.0f} TF), Gemm {out['gemm_us']:.1f} us ({out['gemm_tflops']:.0f} TF), "
-        f"SkipLN {out['skip_layer_norm_us']:.1f} us; selected {[s.rsplit(':', 1)[1] for s in selected]}")
+    log(f"  ffn M={m} H={h} I={i} ({out['engine']} engine): {ms_per_step * 1e3:.1f} us/step; GemmGelu "
+        f"{out['gemm_gelu_us']:.1f} us ({out['gemm_gelu_tflops']:.0f} TF), Gemm {out['gemm_us']:.1f} us "
+        f"({out['gemm_tflops']:.0f} TF), SkipLN {out['skip_layer_norm_us']:.1f} us; selected {out['selected']}")
     return out
 
 
@@ -291,32 +394,136 @@ def bench_attention(args, cache_dir: str) -> dict:
     return out
 
 
-def bench_copy(args, cache_dir: str) -> dict:
+def copy_graph():
     """One Relu over 64 Mi non-negative floats: the relu_fp32 kernel reads and
-    writes exactly 256 MiB each. Its GB/s is the streaming reference for the
-    bandwidth kernels, and its FETCH_SIZE / WRITE_SIZE counters calibrate the
-    HBM traffic figures of the other kernels."""
+    writes exactly 256 MiB each."""
     import numpy as np
 
     from cutriton_amd import workloads
 
-    count = 64 << 20
     g = workloads.GraphSpec()
-    g.inputs["x"] = ((count,), "float32", "")
+    g.inputs["x"] = ((COPY_FLOATS,), "float32", "")
     g.add("copy", "Relu", ["x"], ["y"])
     g.outputs.append("y")
-    x = np.abs(np.random.default_rng(workloads.SEED).standard_normal(count, dtype=np.float32))
+    x = np.abs(np.random.default_rng(workloads.SEED).standard_normal(COPY_FLOATS, dtype=np.float32))
+    return g, x
+
+
+def bench_copy(args, cache_dir: str) -> dict:
+    """The Relu copy's GB/s: the streaming reference for the bandwidth
+    kernels."""
+    g, x = copy_graph()
     ms_per_step, op_kernel_ms, _, ops, _ = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
     kernel_ms = op_kernel_ms[0]
-    out = {"workload": "relu_fp32_64Mi", "bytes": 2 * 4 * count, "kernel_us": kernel_ms * 1e3,
-           "gbps": 2 * 4 * count / (kernel_ms * 1e-3) / 1e9, "ms_per_step": ms_per_step}
+    out = {"workload": "relu_fp32_64Mi", "bytes": 2 * 4 * COPY_FLOATS, "kernel_us": kernel_ms * 1e3,
+           "gbps": 2 * 4 * COPY_FLOATS / (kernel_ms * 1e-3) / 1e9, "ms_per_step": ms_per_step}
     log(f"  copy: {out['kernel_us']:.1f} us, {out['gbps']:.0f} GB/s")
     return out
 
 
-def cpu_baseline(budget_s: float) -> dict:
-    """The same ResNet-50 bs32 graph in PyTorch-CPU FP32, timed for about
-    `budget_s` seconds after one warm-up batch."""
+# --- HBM traffic from rocprofv3 counter passes -------------------------------
+
+
+def counter_pass(cache_dir: str) -> None:
+    """The workload of one counter pass (run under rocprofv3 by
+    measure_traffic): the Relu copy, ResNet-50 bs32 and the FFN at M=4096 on
+    the engines the timed run used, three steps each, tuned choices read from
+    the cache."""
+    import torch
+
+    from cutriton_amd import workloads
+
+    handle = torch.cuda.current_stream().cuda_stream
+    g, x = copy_graph()
+    template, fx = workloads.ffn(FFN_PROFILE["tokens"]["x"][2][0], FFN_SHAPE[1], FFN_SHAPE[2])
+    cases = (
+        (g, {"x": x}, None),
+        (workloads.resnet50(1), {"input": workloads.resnet50_input(32)}, RESNET_PROFILE),
+        (template, {"x": fx[:FFN_SHAPE[0]]}, FFN_PROFILE),
+    )
+    for graph, feeds, profiles in cases:
+        eng, ctx, keep = _context(graph, feeds, cache_dir, False, "use_cache", profiles)
+        for _ in range(3):
+            ctx.run_async(handle)
+            ctx.synchronize()
+        del ctx, eng, keep
+        torch.cuda.synchronize()
+
+
+def _read_counter(path: str) -> dict[str, list[float]]:
+    """Per kernel name, the counter's value of each dispatch (summed over the
+    instances rocprofv3 reports for one dispatch)."""
+    per: dict[str, dict[str, float]] = defaultdict(lambda: defaultdict(float))
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            per[row["Kernel_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
+    return {name: list(values.values()) for name, values in per.items()}
+
+
+def measure_traffic(cache_dir: str) -> dict:
+    """Calibrated HBM bytes per launch of the conv family (ResNet-50 bs32) and
+    of the FFN GEMMs (M=4096), from one FETCH_SIZE and one WRITE_SIZE pass.
+    FETCH_SIZE and WRITE_SIZE count KiB at the L2's memory side; each is
+    scaled by the factor that maps the Relu copy's reading to its known
+    256 MiB."""
+    tool = shutil.which("rocprofv3")
+    if tool is None:
+        return {"error": "rocprofv3 not found"}
+    families = {
+        "conv": lambda k: k.startswith("conv_"),
+        "ffn_gemms": lambda k: k.startswith("gemm") and "fp16" in k,
+    }
+    known_kib = 4 * COPY_FLOATS / 1024
+    result: dict = {"calibration": {}, "kib_per_launch": {f: {} for f in families}}
+    env = dict(os.environ, TMPDIR="/tmp")
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out_dir = tempfile.mkdtemp(prefix=f"cutriton-{counter.lower()}-")
+        cmd = ["timeout", "-s", "KILL", "300", tool, "--pmc", counter, "--output-format", "csv", "-d", out_dir,
+               "-o", "run", "--", sys.executable, "-u", str(ROOT / "bench.py"), "--counter-pass",
+               "--tuning-cache", cache_dir]
+        log(f"  counter pass {counter} ...")
+        t0 = time.perf_counter()
+        with open(os.path.join(out_dir, "rocprofv3.log"), "w") as logf:
+            rc = subprocess.run(cmd, stdout=logf, stderr=subprocess.STDOUT, cwd="/tmp", env=env).returncode
+        files = glob.glob(os.path.join(out_dir, "**", "*counter_collection.csv"), recursive=True)
+        log(f"  counter pass {counter}: exit {rc}, {time.perf_counter() - t0:.1f} s")
+        if not files:
+            return {"error": f"rocprofv3 --pmc {counter} exited {rc} without a counter file"}
+        values = _read_counter(files[0])
+        copy = values.get("relu_fp32")
+        if not copy:
+            return {"error": f"no relu_fp32 dispatch in the {counter} pass"}
+        scale = known_kib / (sum(copy) / len(copy))
+        result["calibration"][counter] = round(scale, 4)
+        for family, match in families.items():
+            samples = [v for name, vs in values.items() if match(name) for v in vs]
+            if not samples:
+                return {"error": f"no {family} dispatch in the {counter} pass"}
+            result["kib_per_launch"][family][counter] = sum(samples) / len(samples) * scale
+        shutil.rmtree(out_dir, ignore_errors=True)
+    result["bytes_per_launch"] = {f: int(round(1024 * sum(v.values()))) for f, v in result["kib_per_launch"].items()}
+    return result
+
+
+# --- CPU baseline ------------------------------------------------------------------
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baselines(budget_s: float) -> dict:
+    """The reference's CPU path on this host: each graph in PyTorch-CPU FP32
+    (FP16 constants and inputs widened), 3 warm-ups, then timed iterations
+    until at least 10 are done and `budget_s` seconds have passed (at most
+    30), median reported."""
+    import numpy as np
     import torch
 
     from cutriton_amd import workloads
@@ -325,34 +532,52 @@ def cpu_baseline(budget_s: float) -> dict:
     cores = os.cpu_count() or 1
     # The host share of one GPU is capped by OMP_NUM_THREADS where it is set.
     torch.set_num_threads(min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
-    batch = 32
-    graph = workloads.resnet50(batch)
-    consts = torch_cpu.prepare(graph)
-    x = torch.from_numpy(workloads.resnet50_input(batch))
-    torch_cpu.run(graph, consts, {"input": x})
-    times = []
-    t_start = time.perf_counter()
-    while not times or (time.perf_counter() - t_start < budget_s and len(times) < 10):
-        t0 = time.perf_counter()
-        torch_cpu.run(graph, consts, {"input": x})
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    cpu_model = ""
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": round(batch / med, 2),
-        "unit": "img/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"ResNet-50 bs32 FP32 PyTorch-CPU restatement of the same graph, {len(times)} batches after 1 "
-                  f"warm-up, median {med:.2f} s/batch; host {cpu_model} ({cores} logical CPUs)",
-    }
+    host = f"{_cpu_model()} ({cores} logical CPUs)"
+
+    def timed(graph, feeds) -> tuple[float, int]:
+        consts = torch_cpu.prepare(graph)
+        tensors = {k: torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32)) for k, v in feeds.items()}
+        for _ in range(CPU_WARMUPS):
+            torch_cpu.run(graph, consts, tensors)
+        times = []
+        start = time.perf_counter()
+        while len(times) < CPU_MIN_ITERATIONS or (time.perf_counter() - start < budget_s and len(times) < 30):
+            t0 = time.perf_counter()
+            torch_cpu.run(graph, consts, tensors)
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2], len(times)
+
+    out: dict = {}
+    for batch in (32, 1, 64):
+        graph = workloads.resnet50(batch)
+        med, n = timed(graph, {"input": workloads.resnet50_input(batch)})
+        out[f"resnet50_bs{batch}"] = {
+            "value": round(batch / med, 2), "unit": "img/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"ResNet-50 bs{batch} FP32, PyTorch-CPU restatement of the same graph, {CPU_WARMUPS} warm-ups "
+                      f"+ {n} timed batches, median {med * 1e3:.1f} ms/batch; host {host}"}
+        log(f"  cpu resnet50 bs{batch}: {med * 1e3:.1f} ms/batch over {n}")
+    for m, h, i in (FFN_SHAPE, FFN_SMALL_SHAPE):
+        graph, x = workloads.ffn(m, h, i)
+        med, n = timed(graph, {"x": x})
+        out[f"ffn_m{m}_h{h}_i{i}"] = {
+            "value": round(2 * 2 * m * h * i / med / 1e12, 4), "unit": "TFLOP/s (two GEMMs)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"FFN M={m} H={h} I={i} in FP32 (FP16 weights and input widened), {CPU_WARMUPS} warm-ups + {n} "
+                      f"timed steps, median {med * 1e3:.2f} ms/step; host {host}"}
+        log(f"  cpu ffn M={m}: {med * 1e3:.2f} ms/step over {n}")
+    graph, x = workloads.conv_bn_relu()
+    med, n = timed(graph, {"x": x})
+    flops = sum(workloads.node_flops(graph).values())
+    out["conv_bn_relu_1x64x56x56"] = {
+        "value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": f"Conv 3x3 + BatchNorm + Relu x[1,64,56,56] FP32, {CPU_WARMUPS} warm-ups + {n} timed runs, median "
+                  f"{med * 1e3:.3f} ms; host {host}"}
+    log(f"  cpu single conv node: {med * 1e3:.3f} ms over {n}")
+    return out
+
+
+def _rounded(d: dict) -> dict:
+    return {k: (round(v, 3) if isinstance(v, float) else v) for k, v in d.items()}
 
 
 def main() -> int:
@@ -363,8 +588,11 @@ def main() -> int:
     parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "norms", "attention", "copy"), default="all")
     parser.add_argument("--tuning-cache", default="",
                         help="tuning cache folder to reuse (default: a fresh temporary folder, so every op is tuned)")
-    parser.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
-                        help="bounded CPU sample; 0 skips the CPU baseline")
+    parser.add_argument("--cpu-baseline-seconds", type=float, default=5.0,
+                        help="time budget per CPU baseline case beyond its 3 warm-ups and 10 iterations; "
+                             "0 skips the CPU baselines")
+    parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    parser.add_argument("--counter-pass", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -375,6 +603,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (cuda:0)", file=sys.stderr)
         return 2
+    if args.counter_pass:
+        counter_pass(args.tuning_cache)
+        return 0
     log(f"device: {torch.cuda.get_device_name(0)}")
     cache_dir = args.tuning_cache or tempfile.mkdtemp(prefix="cutriton-tuning-")
     os.makedirs(cache_dir, exist_ok=True)
@@ -383,35 +614,44 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic (seeded N(0,1) inputs, random-init weights)",
         "config": {"workload": "resnet50_v1.5_fp32_nchw_bs32", "global_batch": 32, "image": [3, 224, 224],
+                   "engine": "dynamic batch profile min1/opt32/max64, hipGraph replay",
                    "parallelism": "single-gpu"},
     }
     if args.workload in ("all", "resnet50"):
-        r = bench_resnet(args, cache_dir)
+        r = bench_resnet(args, cache_dir, 32, profile=True)
         result.update(value=round(r["img_s"], 2), ms_per_step=round(r["ms_per_step"], 4),
                       pct_fp32_mfma_peak=round(r["pct_fp32_mfma_peak"], 2), roofline=r["roofline"])
         result["resnet50_tflops"] = round(r["tflops"], 3)
-        # The profile-max batch of the same graph, on its own tuned engine.
-        r64 = bench_resnet(args, cache_dir, batch=64)
-        result["resnet50_bs64"] = {"img_s": round(r64["img_s"], 2), "ms_per_step": round(r64["ms_per_step"], 4),
+        r64 = bench_resnet(args, cache_dir, 64, profile=True)
+        result["resnet50_bs64"] = {"engine": r64["engine"], "img_s": round(r64["img_s"], 2),
+                                   "ms_per_step": round(r64["ms_per_step"], 4),
                                    "pct_fp32_mfma_peak": round(r64["pct_fp32_mfma_peak"], 2),
                                    "conv_tflops": r64["roofline"]["achieved"]}
+        r1 = bench_resnet(args, cache_dir, 1, profile=False)
+        result["resnet50_bs1"] = {"engine": r1["engine"], "img_s": round(r1["img_s"], 2),
+                                  "ms_per_step": round(r1["ms_per_step"], 4),
+                                  "pct_fp32_mfma_peak": round(r1["pct_fp32_mfma_peak"], 2),
+                                  "conv_tflops": r1["roofline"]["achieved"]}
+        result["conv_bn_relu_node"] = _rounded(bench_single_node(args, cache_dir))
     if args.workload in ("all", "ffn"):
-        f = bench_ffn(args, cache_dir)
-        f.pop("selected", None)
-        result["ffn"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in f.items()}
+        f = bench_ffn(args, cache_dir, FFN_SHAPE, profile=True)
+        result["ffn"] = _rounded(f)
         if args.workload == "ffn":
             result.update(value=round(f["tflops_block"], 3), unit="TFLOP/s", ms_per_step=round(f["ms_per_step"], 4),
-                          dtype="fp16", config={"workload": f["workload"], "parallelism": "single-gpu"})
+                          dtype="fp16", config={"workload": f["workload"], "engine": f["engine"],
+                                                "parallelism": "single-gpu"})
+        result["ffn_m512"] = _rounded(bench_ffn(args, cache_dir, FFN_SMALL_SHAPE, profile=False))
+        result["ffn_m512"].pop("roofline", None)
     if args.workload in ("all", "norms"):
         n = bench_norms(args, cache_dir)
-        result["norms"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in n.items()}
+        result["norms"] = _rounded(n)
         if args.workload == "norms":
             result.update(value=round(n["softmax_gbps"], 1), unit="GB/s", dtype="fp16",
                           ms_per_step=round(n["softmax_us"] * 1e-3, 4),
                           config={"workload": "softmax_fp16_262144x1024", "parallelism": "single-gpu"})
     if args.workload in ("all", "attention"):
         a = bench_attention(args, cache_dir)
-        result["attention"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in a.items()}
+        result["attention"] = _rounded(a)
         if args.workload == "attention":
             result.update(value=round(a["full_tflops"], 3), unit="TFLOP/s", dtype="fp16",
                           ms_per_step=round(a["full_us"] * 1e-3, 4),
@@ -420,8 +660,22 @@ def main() -> int:
         c = bench_copy(args, cache_dir)
         result.update(value=round(c["gbps"], 1), unit="GB/s", ms_per_step=round(c["ms_per_step"], 4),
                       config={"workload": c["workload"], "parallelism": "single-gpu"}, copy=c)
+    if args.workload == "all" and not args.no_traffic:
+        traffic = measure_traffic(cache_dir)
+        result["traffic"] = traffic
+        if "bytes_per_launch" in traffic:
+            for key, family in (("roofline", "conv"), ("ffn", "ffn_gemms")):
+                block = result[key] if key == "roofline" else result[key]["roofline"]
+                block["traffic"] = traffic["bytes_per_launch"][family]
+                block["traffic_vs_algorithmic"] = round(block["traffic"] / block["algorithmic_bytes_per_launch"], 3)
+                block["traffic_source"] = "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE child passes of this run, " \
+                                          "scaled by a 256 MiB copy"
+        else:
+            log(f"  traffic not measured: {traffic.get('error')}")
     if args.cpu_baseline_seconds > 0 and args.workload in ("all", "resnet50"):
-        result["cpu_baseline"] = cpu_baseline(args.cpu_baseline_seconds)
+        cpu = cpu_baselines(args.cpu_baseline_seconds)
+        result["cpu_baseline"] = cpu["resnet50_bs32"]
+        result["cpu_baselines"] = cpu
     print(json.dumps(result), flush=True)
     return 0
 

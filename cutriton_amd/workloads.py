@@ -229,12 +229,11 @@ def stem_kat(batch_shape: tuple[int, ...] = (1, 3, 224, 224)) -> tuple[GraphSpec
     return g, x, expected
 
 
-def node_flops(spec: GraphSpec) -> dict[str, int]:
-    """Algorithmic FLOPs (2 x multiply-accumulates) of every Conv and Gemm node,
-    by name; BatchNorm, activations, pooling and adds count zero."""
+def value_shapes(spec: GraphSpec) -> dict[str, tuple[int, ...]]:
+    """The shape of every value of `spec` (inputs, constants and node
+    outputs), by name, for the node types the workloads use."""
     shapes = {name: tuple(shape) for name, (shape, _, _) in spec.inputs.items()}
     shapes.update({name: tuple(arr.shape) for name, (arr, _) in spec.constants.items()})
-    flops: dict[str, int] = {}
     for node in spec.nodes:
         a, ins = node.attributes, [shapes[i] for i in node.inputs]
         if node.op_type == "Conv":
@@ -243,7 +242,6 @@ def node_flops(spec: GraphSpec) -> dict[str, int]:
             p = (h + pd[0] + pd[2] - dl[0] * (r - 1) - 1) // st[0] + 1
             q = (w + pd[1] + pd[3] - dl[1] * (s - 1) - 1) // st[1] + 1
             out = (n, k, p, q)
-            flops[node.name] = 2 * n * k * c * r * s * p * q
         elif node.op_type == "MaxPool":
             (n, c, h, w), ker = ins[0], a["kernel_shape"]
             st, pd = a.get("strides", ker), a.get("pads", [0, 0, 0, 0])
@@ -253,10 +251,24 @@ def node_flops(spec: GraphSpec) -> dict[str, int]:
         elif node.op_type == "Flatten":
             out = (ins[0][0], int(np.prod(ins[0][1:])))
         elif node.op_type == "Gemm":
-            (m, k), (_, n) = ins[0], ins[1]
-            out = (m, n)
-            flops[node.name] = 2 * m * n * k
+            out = (ins[0][0], ins[1][1])
         else:
             out = ins[0]
         shapes[node.outputs[0]] = out
+    return shapes
+
+
+def node_flops(spec: GraphSpec) -> dict[str, int]:
+    """Algorithmic FLOPs (2 x multiply-accumulates) of every Conv and Gemm node,
+    by name; BatchNorm, activations, pooling and adds count zero."""
+    shapes = value_shapes(spec)
+    flops: dict[str, int] = {}
+    for node in spec.nodes:
+        if node.op_type == "Conv":
+            (_, c, _, _), (_, _, r, s) = shapes[node.inputs[0]], shapes[node.inputs[1]]
+            n, k, p, q = shapes[node.outputs[0]]
+            flops[node.name] = 2 * n * k * c * r * s * p * q
+        elif node.op_type == "Gemm":
+            (m, k), (_, n) = shapes[node.inputs[0]], shapes[node.inputs[1]]
+            flops[node.name] = 2 * m * n * k
     return flops
