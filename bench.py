@@ -585,7 +585,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=("all", "resnet50", "ffn", "norms", "attention", "copy"), default="all")
+    parser.add_argument("--workload", choices=("all", "resnet50", "resnet50_bs32", "ffn", "norms", "attention", "copy"),
+                        default="all", help="resnet50_bs32: only the batch-32 leg of resnet50")
     parser.add_argument("--tuning-cache", default="",
                         help="tuning cache folder to reuse (default: a fresh temporary folder, so every op is tuned)")
     parser.add_argument("--cpu-baseline-seconds", type=float, default=5.0,
@@ -617,11 +618,12 @@ def main() -> int:
                    "engine": "dynamic batch profile min1/opt32/max64, hipGraph replay",
                    "parallelism": "single-gpu"},
     }
-    if args.workload in ("all", "resnet50"):
+    if args.workload in ("all", "resnet50", "resnet50_bs32"):
         r = bench_resnet(args, cache_dir, 32, profile=True)
         result.update(value=round(r["img_s"], 2), ms_per_step=round(r["ms_per_step"], 4),
                       pct_fp32_mfma_peak=round(r["pct_fp32_mfma_peak"], 2), roofline=r["roofline"])
         result["resnet50_tflops"] = round(r["tflops"], 3)
+    if args.workload in ("all", "resnet50"):
         r64 = bench_resnet(args, cache_dir, 64, profile=True)
         result["resnet50_bs64"] = {"engine": r64["engine"], "img_s": round(r64["img_s"], 2),
                                    "ms_per_step": round(r64["ms_per_step"], 4),

@@ -32,14 +32,13 @@
 // completed, one atomic increment of the tile's counter tells the workgroup
 // whether it is the last of the tile. The last one reads all shares back and
 // adds them in split order (0, 1, ..., SPLIT-1: the result does not depend on
-// arrival order),
-// applies the epilogue and resets the counter to zero for the next launch.
-// Nothing waits on another workgroup, and no cache-wide write-back is needed:
-// only the shares travel through the coherent level.
+// arrival order), applies the epilogue and resets the counter to zero for the
+// next launch. Nothing waits on another workgroup.
 //
 // LDS holds both operands depth-contiguous, A as [m][d] and B as [j][d]
-// (rows padded by 4 floats, which keeps the 16 lanes of a read phase on
-// distinct banks), so one 16-byte read gives a lane four depths. A 16x16x4
+// (rows padded by 4 floats; gfx950 serves these 16-byte reads at 256 B and
+// the 16-byte writes at 128 B per LDS cycle, padded or not, with no
+// bank-conflict cycles), so one 16-byte read gives a lane four depths. A 16x16x4
 // MFMA takes depth slot q = lane / 16 from every lane; within a depth tile
 // the steps take the depths in the order
 //   step 4g + e, lane quarter q  ->  depth 16g + 4q + e
@@ -518,7 +517,29 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
         for (int t = 0; t < TN; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) StoreShared(mine + ((i * TN + t) * 4 + r) * 64 + lane, acc[i][t][r]);
-      // The shares must have reached the coherent level before the count.
+      // Ordering of the hand-off. The shares are stored and loaded with
+      // agent-scope atomics, which gfx950 issues with the device-coherence
+      // bit (sc1): a store is written through to the device's coherence
+      // point, and its vmcnt decrement comes back once it is there; a load
+      // is served at that point, never from a stale L1 or L2 line. The
+      // count is an agent-scope read-modify-write: its updates form one
+      // order for the whole device.
+      //  1. Each wave waits (vmcnt 0) until its share stores are at the
+      //     coherence point; the barrier then holds thread 0 until every wave
+      //     has waited, so the whole share is visible before the count.
+      //  2. The workgroup that reads SPLIT - 1 comes after every other
+      //     share's count in that order, hence after its stores.
+      //  3. Thread 0 waits for the count's return value before it writes the
+      //     flag, and the second barrier orders the flag before every share
+      //     load, so no share load is issued before the count has returned.
+      //  4. The counter's relaxed reset is ordered for the next launch by the
+      //     kernel boundary.
+      // In the language memory model these relaxed atomics order nothing
+      // across locations; a release on the count and an acquire fence in the
+      // last workgroup would. On gfx950 those become a write-back and an
+      // invalidate of the whole L2 per workgroup, which made the ResNet-50
+      // step 5 % slower (the tuner then dropped split-K for most layers), so
+      // the hand-off relies on the ordering above instead.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       unsigned* flag = reinterpret_cast<unsigned*>(smem);
