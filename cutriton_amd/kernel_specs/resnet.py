@@ -301,9 +301,18 @@ def register_bandwidth_kernels() -> None:
     ) + reserved()
     register(KernelSpec(
         "max_pool.fp32.nchw", "MaxPool", 1, "pool_fp32.hip", pool_arguments,
-        # One workgroup per (image, channel) plane and band of 8 output rows.
-        (mul(mul(output_dim(0), output_dim(1)), ceil_div(output_dim(2), literal(8))),),
-        variants("max_pool_fp32_nchw"), layout="NCHW",
+        # One workgroup per GROUP_BANDS bands of BAND output rows of one
+        # (image, channel) plane.
+        (ceil_div(mul(mul(output_dim(0), output_dim(1)), ceil_div(output_dim(2), meta("BAND"))),
+                  meta("GROUP_BANDS")),),
+        tuple(KernelVariant(name, symbol, num_warps=4, meta={"BAND": band, "GROUP_BANDS": group},
+                            default=name == "w4")
+              for name, symbol, band, group in (
+                  ("w4", "max_pool_fp32_nchw", 8, 1),
+                  ("b16g4", "max_pool_fp32_nchw_b16g4", 16, 4),
+                  # 3 x 3 / 2 windows without LDS; other shapes as bands of 8
+                  ("d8", "max_pool_fp32_nchw_d8", 8, 8))),
+        layout="NCHW",
     ))
 
     gap_arguments = (

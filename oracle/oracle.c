@@ -9,7 +9,8 @@
  * named beside it (python/cutriton/triton_kernels/...):
  *   ct_oracle_conv2d          resnet.py:88-114   (zero padding, dilation)
  *   ct_oracle_batch_norm      resnet.py:117-130  ((x-mean)/sqrt(var+eps)*scale+bias)
- *   ct_oracle_max_pool        resnet.py:159-182  (-inf outside the image)
+ *   ct_oracle_max_pool        resnet.py:159-182  (-inf outside the image; NaN never
+ *                             selected; +0 above -0)
  *   ct_oracle_global_avg_pool resnet.py:185-198  (sum / (H*W))
  *   ct_oracle_gemm            resnet.py:201-213, transformer.py:17-60 (+ bias[n])
  *   ct_oracle_gelu            transformer.py:110-116 (0.5 x (1 + erf(x/sqrt 2)))
@@ -87,7 +88,11 @@ void ct_oracle_max_pool(const double* x, int n, int c, int h, int w, int kernel_
             const int iw = ow * stride_w - pad_w + kw * dil_w;
             if (iw < 0 || iw >= w) continue;
             const double v = src[(size_t)ih * w + iw];
-            if (v > best) best = v;
+            /* tl.maximum(accumulator, v) of resnet.py:178-180 (maxNum: a NaN
+             * never wins, so an all-NaN window keeps the -inf start); a tie of
+             * zeros takes +0 (IEEE 754-2019 maximumNumber; maxNum leaves it
+             * unspecified). */
+            if (v > best || (v == 0.0 && best == 0.0 && signbit(best) && !signbit(v))) best = v;
           }
         }
         out[((size_t)plane * out_h + oh) * out_w + ow] = best;

@@ -288,6 +288,40 @@ def test_max_pool_bit_exact(shape, kernel, stride, pad):
     assert np.array_equal(out["y"].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("variant", ["w4", "b16g4", "d8"])
+@pytest.mark.parametrize("shape,kernel,stride,pad", [
+    ((2, 8, 112, 112), 3, 2, 1),    # stem pool: even/odd split rows
+    ((1, 3, 20, 24), 3, 1, 1),      # stride 1: plain staged rows
+    ((1, 2, 17, 14), 3, 2, 1),      # rows not whole float4s: global reads
+    ((1, 2, 9, 16), 2, 2, 0),       # even window, no padding, split rows
+    ((1, 3, 15, 16), 3, 2, 1),      # odd height: the last window hangs below the image
+])
+def test_max_pool_special_values(tmp_path, variant, shape, kernel, stride, pad):
+    """Bit-exact against the oracle on inputs full of NaN, +-inf and +-0:
+    NaN never wins (an all-NaN window gives -inf), +0 beats -0."""
+    rng = np.random.default_rng(17)
+    specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.5, -2.0], dtype=np.float32)
+    x = rng.standard_normal(shape, dtype=np.float32)
+    mask = rng.random(shape) < 0.6
+    x[mask] = rng.choice(specials, size=int(mask.sum()))
+    x[0, 0, :4, :4] = np.nan                    # all-NaN windows
+    x[0, -1, -4:, -4:] = -0.0                   # windows of -0 only
+    x[0, -1, -4:, -2] = 0.0                     # and with a +0 among them
+    g = workloads.GraphSpec()
+    g.inputs["x"] = (shape, "float32", "NCHW")
+    g.add("pool", "MaxPool", ["x"], ["y"], kernel_shape=[kernel, kernel], strides=[stride, stride],
+          pads=[pad] * 4, dilations=[1, 1])
+    g.outputs.append("y")
+    kid = "max_pool.fp32.nchw"
+    pack = filtered_pack(tmp_path / "pack", lambda e: e["kernel_id"] != kid or e["variant_id"] == variant)
+    out, eng, _ = run_graph(g, {"x": x}, engine.CompileOptions(kernel_artifact_dir=pack, tuning_mode="disabled"))
+    op = eng.ops()[0]
+    assert op.candidates[op.selected_candidate].endswith(f"{kid}:{variant}"), op
+    want = oracle.evaluate(g, {"x": x})["y"].astype(np.float32)
+    assert not np.isnan(want).any()
+    assert np.array_equal(out["y"].view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("shape", [(2, 2048, 7, 7), (3, 5, 1, 1), (1, 3, 60, 61), (1, 300, 8, 8), (1, 70, 7, 7)])
 @pytest.mark.parametrize("variant", ["w4", "p16"])
 def test_global_average_pool(tmp_path, shape, variant):

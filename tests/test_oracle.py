@@ -119,6 +119,38 @@ def test_max_pool_padding_is_minus_infinity():
     assert got[0, 0, 0, 0] == x[0, 0, :2, :2].max()
 
 
+def test_max_pool_special_values():
+    """NaN never wins (the window max of the numbers, -inf for an all-NaN
+    window), +0 beats -0 in either order, infinities order as numbers."""
+    nan, inf = math.nan, math.inf
+    x = np.array([[nan, 1.0, -inf, nan],
+                  [nan, nan, -0.0, 0.0],
+                  [inf, -1.0, 0.0, -0.0],
+                  [-inf, -inf, -0.0, -0.0]]).reshape(1, 1, 4, 4)
+    got = oracle.max_pool(x, (2, 2), (2, 2))[0, 0]
+    assert got[0, 0] == 1.0                        # NaNs skipped
+    assert got[0, 1] == 0.0 and not math.copysign(1.0, got[0, 1]) < 0   # -inf, nan, -0, +0 -> +0
+    assert got[1, 0] == inf
+    assert got[1, 1] == 0.0 and not math.copysign(1.0, got[1, 1]) < 0   # +0 first, then -0 -> +0
+    allnan = oracle.max_pool(np.full((1, 1, 2, 2), nan), (2, 2), (2, 2))
+    assert allnan[0, 0, 0, 0] == -inf
+    negzero = oracle.max_pool(np.full((1, 1, 2, 2), -0.0), (2, 2), (2, 2))
+    assert negzero[0, 0, 0, 0] == 0.0 and math.copysign(1.0, negzero[0, 0, 0, 0]) < 0
+    # Brute force on a random mix: nanmax of each window (NaN windows: -inf),
+    # with the zero tie resolved to +0.
+    g = rng(11)
+    pool = np.array([nan, inf, -inf, 0.0, -0.0, 1.5, -2.0])
+    x = g.choice(pool, size=(2, 3, 7, 8))
+    got = oracle.max_pool(x, (3, 3), (2, 2), (1, 1, 1, 1))
+    for (b, ch, oh, ow), v in np.ndenumerate(got):
+        window = [x[b, ch, ih, iw] for ih in range(2 * oh - 1, 2 * oh + 2) for iw in range(2 * ow - 1, 2 * ow + 2)
+                  if 0 <= ih < 7 and 0 <= iw < 8 and not math.isnan(x[b, ch, ih, iw])]
+        want = max(window, default=-inf)
+        if want == 0.0:
+            want = 0.0 if any(math.copysign(1.0, z) > 0 for z in window if z == 0.0) else -0.0
+        assert v == want and math.copysign(1.0, v) == math.copysign(1.0, want), (b, ch, oh, ow)
+
+
 def test_global_average_pool_and_gemm_vs_numpy():
     g = rng(5)
     x = g.standard_normal((3, 7, 7, 7))
