@@ -390,10 +390,21 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   // Residual of the lane's outputs (residual-join epilogue without split-K):
   // loaded before the last depth tile is multiplied, so its latency hides
   // behind those MFMAs instead of stalling the epilogue.
+  // Staged epilogue: when an image's output plane is a whole number of
+  // 16-byte groups (P*Q % 4 == 0), the finished tile goes through LDS so that
+  // every lane reads its residual and writes its output as 16 bytes of four
+  // consecutive pixels of one channel, a wavefront covering whole 256-byte
+  // runs, instead of four 4-byte values of four channels.
+  constexpr int SROW = BN + 4;  // staged row: BN outputs of one channel, padded
+  constexpr int SGROUPS = BN / 4;
+  constexpr int SITEMS = BM * SGROUPS / THREADS;  // 16-byte groups per thread
+  constexpr bool kStagedEpilogue = WGK == 1 && BM * SROW <= L::kTiles && SITEMS * THREADS == BM * SGROUPS;
+  const bool staged_epilogue = kStagedEpilogue && (pq & 3) == 0;
+
   constexpr bool PREFETCH_RESIDUAL = EPI == kBatchNormAddRelu && SPLIT == 1;
   float res_pre[PREFETCH_RESIDUAL ? TM : 1][PREFETCH_RESIDUAL ? TN : 1][4];
   auto prefetch_residual = [&]() {
-    if (!PREFETCH_RESIDUAL || wk != 0) return;
+    if (!PREFETCH_RESIDUAL || wk != 0 || staged_epilogue) return;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int col = n0 + wn + t * 16 + lane16;
@@ -607,6 +618,60 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     }
   }
 
+  if constexpr (kStagedEpilogue) {
+    if (staged_epilogue) {
+      // The residual loads go out first; their latency overlaps the LDS
+      // transpose. Group item = row * SGROUPS + cg: channel m0 + row,
+      // columns n0 + 4 cg .. + 3, all in one image (P*Q % 4 == 0); its
+      // offset is recomputed after the transpose rather than kept live.
+      auto group_at = [&](int item, bool& ok) -> size_t {
+        const int row = item / SGROUPS;
+        const int col = n0 + 4 * (item - row * SGROUPS);
+        const int m = m0 + row;
+        ok = m < g.k && col < columns;  // columns % 4 == 0: a group is whole or outside
+        const int cimg = ok ? col / pq : 0;
+        return ok ? (static_cast<size_t>(cimg) * g.k + m) * pq + (col - cimg * pq) : 0;
+      };
+      f32x4 res[EPI == kBatchNormAddRelu ? SITEMS : 1];
+      if constexpr (EPI == kBatchNormAddRelu) {
+#pragma unroll
+        for (int it = 0; it < SITEMS; ++it) {
+          bool ok;
+          const size_t at = group_at(tid + it * THREADS, ok);
+          res[it] = ok ? *reinterpret_cast<const f32x4*>(residual + at) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      }
+      __syncthreads();  // the LDS tiles (and the split-K flag) are free
+      float* stage = smem;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) stage[(wm + i * 16 + 4 * quarter + r) * SROW + wn + t * 16 + lane16] = acc[i][t][r];
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < SITEMS; ++it) {
+        const int item = tid + it * THREADS;
+        const int row = item / SGROUPS;
+        const int cg = item - row * SGROUPS;
+        bool ok;
+        const size_t at = group_at(item, ok);
+        f32x4 v = *reinterpret_cast<const f32x4*>(stage + row * SROW + 4 * cg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (EPI == kBatchNorm || EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) {
+            v[e] = fmaf(v[e], epi_mul[row], epi_add[row]);
+          }
+          if (EPI == kBatchNormAddRelu) v[e] += res[EPI == kBatchNormAddRelu ? it : 0][e];
+          if (EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v[e] = fmaxf(v[e], 0.0f);
+          if (EPI == kColumnBias) v[e] += bias[n0 + 4 * cg + e];
+        }
+        if (ok) *reinterpret_cast<f32x4*>(output + at) = v;
+      }
+      return;
+    }
+  }
   store_output(from_acc);
 }
 
@@ -641,44 +706,44 @@ __device__ __forceinline__ ConvGeometry MakeGeometry(int n, int c, int h, int w,
     ConvCore<BM, BN, BK, WGM, WGN, WGK, EPI, false>(smem, __VA_ARGS__);                      \
   }
 
-#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK)                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_relu_fp32_##NAME(                     \
-      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
-      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
+#define CT_DEFINE_CONV_VARIANTS(NAME, BM, BN, BK, WGM, WGN, WGK, MIN_GROUPS)                            \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK, MIN_GROUPS) conv_bn_relu_fp32_##NAME(          \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,    \
+      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormRelu, x, weight, scale, bias, mean, variance,      \
-                nullptr, output, CT_CONV_GEOMETRY, epsilon)                                              \
-  }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_fp32_##NAME(                          \
-      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
-      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                 \
+                nullptr, output, CT_CONV_GEOMETRY, epsilon)                                             \
+  }                                                                                                     \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK, MIN_GROUPS) conv_bn_fp32_##NAME(               \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,    \
+      const float* variance, float* output, CT_CONV_DIMS, float epsilon, void*, void*) {                \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNorm, x, weight, scale, bias, mean, variance, nullptr, \
-                output, CT_CONV_GEOMETRY, epsilon)                                                       \
-  }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_bn_add_relu_fp32_##NAME(                 \
-      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
-      const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon, void*,   \
-      void*) {                                                                                           \
+                output, CT_CONV_GEOMETRY, epsilon)                                                      \
+  }                                                                                                     \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK, MIN_GROUPS) conv_bn_add_relu_fp32_##NAME(      \
+      const float* x, const float* weight, const float* scale, const float* bias, const float* mean,    \
+      const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon, void*,  \
+      void*) {                                                                                          \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kBatchNormAddRelu, x, weight, scale, bias, mean, variance,   \
-                residual, output, CT_CONV_GEOMETRY, epsilon)                                             \
-  }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK) conv_fp32_##NAME(const float* x,                \
-                                                              const float* weight, float* output,        \
-                                                              CT_CONV_DIMS, void*, void*) {              \
+                residual, output, CT_CONV_GEOMETRY, epsilon)                                            \
+  }                                                                                                     \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN * WGK, MIN_GROUPS) conv_fp32_##NAME(const float* x,   \
+                                                              const float* weight, float* output,       \
+                                                              CT_CONV_DIMS, void*, void*) {             \
     CT_DISPATCH(BM, BN, BK, WGM, WGN, WGK, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr,       \
-                nullptr, output, CT_CONV_GEOMETRY, 0.0f)                                                 \
+                nullptr, output, CT_CONV_GEOMETRY, 0.0f)                                                \
   }
 
-// name, BM, BN, BK, WGM, WGN, WGK
-CT_DEFINE_CONV_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1)
-CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2)
-CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2)
-CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1)
-CT_DEFINE_CONV_VARIANTS(m32n128, 32, 128, 32, 1, 4, 1)
+// name, BM, BN, BK, WGM, WGN, WGK, workgroups per CU the registers must allow
+CT_DEFINE_CONV_VARIANTS(m128n128, 128, 128, 32, 2, 2, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2, 1)
+CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1, 4)
+CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1, 4)
+CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m32n128, 32, 128, 32, 1, 4, 1, 1)
 
 // Split-K entry points: the first reserved argument is the runtime scratch
 // (kSplitCounterBytes + kSplitShareBytes, zero-initialised by the engine).
