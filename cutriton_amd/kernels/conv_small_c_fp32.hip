@@ -129,15 +129,41 @@ __device__ __forceinline__ void SmallCConv(const float* __restrict__ x, const fl
     }
   }
   if (staged) {
-    for (int row = wv; row < c * rows_in; row += kThreads / 64) {
-      const int ci = row / rows_in;
-      const int ih = ih0 + row - ci * rows_in;
-      const bool row_in = static_cast<unsigned>(ih) < static_cast<unsigned>(h);
-      const float* src = x_img + (static_cast<size_t>(ci) * h + (row_in ? ih : 0)) * w;
-      float* dst = patch + row * cols_in;
-      for (int cc = lane; cc < cols_in; cc += 64) {
-        const int iw = iw0 + cc;
-        dst[cc] = (row_in && static_cast<unsigned>(iw) < static_cast<unsigned>(w)) ? src[iw] : 0.0f;
+    // Patch rows (c, kernel row) go to the wavefronts in turn, a lane per
+    // column. Each wavefront issues the loads of kBatchRows of its rows
+    // before it stores any (raw buffer loads: a position outside the image
+    // reads 0), so a batch costs one memory latency instead of one per row.
+    constexpr int kBatchRows = 4;
+    constexpr int kColSteps = 4;  // columns lane + 64 j, j < kColSteps
+    const __amdgpu_buffer_rsrc_t x_res = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x_img), 0, c * h * w * 4, kBufferFlags);
+    const int rows_total = c * rows_in;
+    for (int col0 = 0; col0 < cols_in; col0 += 64 * kColSteps) {
+      for (int row0 = wv; row0 < rows_total; row0 += (kThreads / 64) * kBatchRows) {
+        float v[kBatchRows][kColSteps];
+#pragma unroll
+        for (int b = 0; b < kBatchRows; ++b) {
+          const int row = row0 + b * (kThreads / 64);
+          const int ci = row / rows_in;
+          const int ih = ih0 + row - ci * rows_in;
+          const bool row_ok = row < rows_total && static_cast<unsigned>(ih) < static_cast<unsigned>(h);
+#pragma unroll
+          for (int j = 0; j < kColSteps; ++j) {
+            const int iw = iw0 + col0 + lane + 64 * j;
+            const bool ok = row_ok && static_cast<unsigned>(iw) < static_cast<unsigned>(w);
+            v[b][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                    x_res, ok ? ((ci * h + ih) * w + iw) * 4 : kNoRead, 0, 0));
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kBatchRows; ++b) {
+          const int row = row0 + b * (kThreads / 64);
+#pragma unroll
+          for (int j = 0; j < kColSteps; ++j) {
+            const int cc = col0 + lane + 64 * j;
+            if (row < rows_total && cc < cols_in) patch[row * cols_in + cc] = v[b][j];
+          }
+        }
       }
     }
   }
