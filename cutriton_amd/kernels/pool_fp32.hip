@@ -332,16 +332,33 @@ __device__ __forceinline__ void GlobalAveragePoolPlanes(const float* __restrict_
   const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * kPlanes;
   const int count = first >= planes ? 0 : static_cast<int>(planes - first < kPlanes ? planes - first : kPlanes);
   const bool staged = spatial <= kMaxSpan;
-  if (staged) {
+  if (staged && count > 0) {
+    // All of a lane's loads are issued before its first LDS store (a lane
+    // past the span re-reads the span's last element), so the span costs
+    // one memory latency.
     const float* src = x + first * spatial;
     const int total = count * spatial;
-    for (int i = lane; i < total; i += 64) span[wave][i] = src[i];
+    constexpr int kPerLane = kPlanes * kMaxSpan / 64;
+    float v[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) v[j] = src[min(lane + 64 * j, max(total - 1, 0))];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      if (lane + 64 * j < total) span[wave][lane + 64 * j] = v[j];
   }
   __syncthreads();
-  if (lane < count) {
-    const float* mine = staged ? &span[wave][lane * spatial] : x + (first + lane) * spatial;
+  // Unrolled so that eight reads are in flight; the adds stay in increasing
+  // spatial order. The LDS and global sources are separate loops: behind
+  // one pointer that may be either, the LDS reads compile to generic (FLAT)
+  // loads.
+  auto plane_sum = [&](const auto* mine) {
     float sum = 0.0f;
+#pragma unroll 8
     for (int i = 0; i < spatial; ++i) sum += mine[i];
+    return sum;
+  };
+  if (lane < count) {
+    const float sum = staged ? plane_sum(&span[wave][lane * spatial]) : plane_sum(x + (first + lane) * spatial);
     output[first + lane] = sum / static_cast<float>(spatial);
   }
 }
