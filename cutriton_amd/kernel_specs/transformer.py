@@ -88,14 +88,37 @@ def gemm_variants(prefix: str) -> tuple[KernelVariant, ...]:
     )
 
 
+# Split-K weight-transposed tiles: SPLIT workgroups per output tile, each on
+# an equal share of the depth, with FP32 shares and per-tile counters in the
+# runtime scratch (16384 counters, then at most 128 MiB of shares). (variant
+# id, BLOCK_M, BLOCK_N, BLOCK_K, wavefronts, SPLIT)
+GEMM_NT_SPLIT_TILES = (
+    ("m64n64s2", 64, 64, 64, 4, 2),
+    ("m64n64s4", 64, 64, 64, 4, 4),
+    ("m128n64s4", 128, 64, 64, 8, 4),
+    ("m128n128s2", 128, 128, 64, 8, 2),
+)
+GEMM_SPLIT_SCRATCH_BYTES = 16384 * 4 + (128 << 20)
+# ceil(M / BLOCK_M) * ceil(N / BLOCK_N) tiles, SPLIT workgroups each.
+GEMM_NT_GRID = (mul(GEMM_GRID[0], meta("SPLIT")),)
+
+
 def gemm_nt_variants(prefix: str) -> tuple[KernelVariant, ...]:
-    return tuple(
+    whole = tuple(
         KernelVariant(
             name, f"{prefix}_{name}", num_warps=waves,
-            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk}, default=name == GEMM_NT_DEFAULT,
+            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk, "SPLIT": 1}, default=name == GEMM_NT_DEFAULT,
         )
         for name, bm, bn, bk, waves in GEMM_NT_TILES
     )
+    split = tuple(
+        KernelVariant(
+            name, f"{prefix}_{name}", num_warps=waves,
+            meta={"BLOCK_M": bm, "BLOCK_N": bn, "BLOCK_K": bk, "SPLIT": sp}, scratch_bytes=GEMM_SPLIT_SCRATCH_BYTES,
+        )
+        for name, bm, bn, bk, waves, sp in GEMM_NT_SPLIT_TILES
+    )
+    return whole + split
 
 
 def register_gemms() -> None:
@@ -127,7 +150,8 @@ def register_gemms() -> None:
                 for i, name in enumerate(inputs)
             ) + (arg("output", "*fp16", "output", index=0),) + GEMM_DIMS + reserved()
             register(KernelSpec(
-                kernel_id + suffix, op_type, 1, source, arguments, GEMM_GRID, variants,
+                kernel_id + suffix, op_type, 1, source, arguments,
+                GEMM_NT_GRID if source == GEMM_NT_SOURCE else GEMM_GRID, variants,
                 dtype="float16", constraints=constraints,
             ))
 

@@ -55,6 +55,12 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufferFlags = 0x00020000;  // gfx9-family raw 32-bit buffer
 constexpr int kNoRead = 0x80000000;       // at or beyond every resource's range: reads 0
 
+// Runtime scratch of the split-K variants: 16384 tile counters, then the
+// FP32 shares (at most 128 MiB).
+constexpr int kSplitMaxTiles = 16384;
+constexpr long long kSplitCounterBytes = kSplitMaxTiles * 4LL;
+constexpr long long kSplitShareBytes = 128LL << 20;
+
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
@@ -131,10 +137,20 @@ struct NtShape {
 // of every stage for the whole output tile, so each wavefront's tile is
 // WAVES_K times larger (fewer LDS fragment reads per MFMA), and the groups'
 // partial sums are added through the idle LDS ring after the last stage.
-template <int BM, int BN, int BK, int STAGES, int WAVES_M, int WAVES_N, bool GELU, bool BIAS, bool VEC, int WAVES_K = 1>
+//
+// SPLIT > 1 gives SPLIT workgroups one output tile, each multiplying an
+// equal share of the depth tiles. Each writes its FP32 share to the runtime
+// scratch; the last to arrive adds the shares in split order (0, 1, ...:
+// the result does not depend on arrival order) and runs the epilogue. The
+// hand-off is the one of the split-K convolutions (conv_fp32.hip, where its
+// ordering argument is written out): agent-scope atomic stores of the
+// shares, a wait for their completion, a barrier, one agent-scope count.
+template <int BM, int BN, int BK, int STAGES, int WAVES_M, int WAVES_N, bool GELU, bool BIAS, bool VEC, int WAVES_K = 1,
+          int SPLIT = 1>
 __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float16* __restrict__ a,
                                            const _Float16* __restrict__ bt, const _Float16* __restrict__ bias,
-                                           _Float16* __restrict__ output, const int m, const int n, const int k) {
+                                           _Float16* __restrict__ output, const int m, const int n, const int k,
+                                           void* __restrict__ scratch = nullptr) {
   using S = NtShape<BM, BN, BK, STAGES>;
   constexpr int CH = S::kChunks;
   constexpr int RPL = S::kRowsPerLoad;
@@ -153,6 +169,7 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 16x16 MFMA tile");
   static_assert(LOADS * RPL * WAVES == BM + BN && BM % RPL == 0, "loads split evenly; none straddles A and B");
   static_assert(2 * LOADS < 64, "vmcnt range");
+  static_assert(SPLIT == 1 || WAVES_K == 1, "split-K keeps each stage's depth in one workgroup");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -163,7 +180,10 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   constexpr int GROUP_M = 8;
   const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = (n + BN - 1) / BN;
-  const int tile = ct::XcdContiguousIndex(blockIdx.x, tiles_m * tiles_n);
+  // Split-K: the SPLIT shares of a tile take adjacent slots (one XCD).
+  const int slot = ct::XcdContiguousIndex(blockIdx.x, tiles_m * tiles_n * SPLIT);
+  const int tile = slot / SPLIT;
+  const int split = slot - tile * SPLIT;
   const int group_width = GROUP_M * tiles_n;
   const int group = tile / group_width;
   const int first_m = group * GROUP_M;
@@ -282,17 +302,72 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
     }
   };
 
-  const int k_tiles = (k + BK - 1) / BK;
+  // This workgroup's depth tiles [kb, ke): all of them, or its share. When
+  // the shares would not fit the scratch, share 0 takes the whole depth and
+  // the others leave.
+  const int k_tiles_all = (k + BK - 1) / BK;
+  const bool split_fits = SPLIT > 1 && tiles_m * tiles_n <= kSplitMaxTiles &&
+                          static_cast<long long>(tiles_m) * tiles_n * SPLIT * BM * BN * 4 <= kSplitShareBytes;
+  if (SPLIT > 1 && !split_fits && split != 0) return;
+  const int per_split = split_fits ? (k_tiles_all + SPLIT - 1) / SPLIT : k_tiles_all;
+  const int kb = min(k_tiles_all, split * per_split);
+  const int ke = min(k_tiles_all, kb + per_split);
+  const int k_tiles = ke - kb;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
-    if (s < k_tiles) load_tile(s, s);
+    if (s < k_tiles) load_tile(s, kb + s);
   for (int kt = 0; kt < k_tiles; ++kt) {
     wait_tile(min(STAGES - 2, k_tiles - 1 - kt));
     // After the barrier every wavefront's loads of tile kt have landed and
     // every wavefront is done with tile kt - 1, whose stage takes the next load.
     __syncthreads();
-    if (kt + STAGES - 1 < k_tiles) load_tile((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+    if (kt + STAGES - 1 < k_tiles) load_tile((kt + STAGES - 1) % STAGES, kb + kt + STAGES - 1);
     compute_tile(kt % STAGES);
+  }
+
+  if (SPLIT > 1 && split_fits) {
+    // Scratch: one counter per tile, then [tile][split][wave][register][lane]
+    // FP32 shares.
+    unsigned* counters = static_cast<unsigned*>(scratch);
+    float* shares = reinterpret_cast<float*>(static_cast<char*>(scratch) + kSplitCounterBytes) +
+                    static_cast<size_t>(tile) * SPLIT * BM * BN;
+    constexpr int WAVE_REGS = TN * TM * 4 * 64;
+    float* mine = shares + static_cast<size_t>(split) * BM * BN + wave * WAVE_REGS;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __hip_atomic_store(mine + ((t * TM + i) * 4 + r) * 64 + lane, acc[t][i][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // every share store has completed; the LDS ring is idle
+    unsigned* flag = reinterpret_cast<unsigned*>(lds);
+    if (tid == 0) *flag = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*flag != SPLIT - 1) return;
+    if (tid == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float* base = shares + wave * WAVE_REGS + lane;
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const float* block = base + (t * TM + i) * 4 * 64;
+        float sum[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] = __hip_atomic_load(const_cast<float*>(block + r * 64), __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int sp = 1; sp < SPLIT; ++sp)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sum[r] += __hip_atomic_load(const_cast<float*>(block + static_cast<size_t>(sp) * BM * BN + r * 64),
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][i][r] = sum[r];
+      }
+    __syncthreads();  // the flag word is read by every thread before the epilogue reuses the ring
   }
 
   // Depth groups: group 0 adds the partial sums of groups 1..WAVES_K-1,
@@ -424,37 +499,45 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
 }  // namespace
 
 // Entry point body: one LDS allocation shared by the two loader paths.
-#define CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, GELU, BIAS, BIAS_PTR)                                     \
-  __shared__ u32x4 lds[NtShape<BM, BN, BK, ST>::kLdsChunks];                                                  \
-  if ((k & 7) == 0) {                                                                                         \
-    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, true, WK>(lds, a, bt, BIAS_PTR, output, m, n, k);          \
-  } else {                                                                                                    \
-    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, false, WK>(lds, a, bt, BIAS_PTR, output, m, n, k);         \
+#define CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, SP, GELU, BIAS, BIAS_PTR)                                   \
+  __shared__ u32x4 lds[NtShape<BM, BN, BK, ST>::kLdsChunks];                                                   \
+  if ((k & 7) == 0) {                                                                                          \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, true, WK, SP>(lds, a, bt, BIAS_PTR, output, m, n, k,       \
+                                                                 scratch);                                     \
+  } else {                                                                                                     \
+    GemmNtCore<BM, BN, BK, ST, WM, WN, GELU, BIAS, false, WK, SP>(lds, a, bt, BIAS_PTR, output, m, n, k,      \
+                                                                  scratch);                                    \
   }
 
-#define CT_DEFINE_GEMM_NT_GROUPS(NAME, BM, BN, BK, ST, WM, WN, WK)                                            \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
-      gemm_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,       \
-                          void*, void*) {                                                                     \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, false, false, nullptr)                                        \
-  }                                                                                                           \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
-      gemm_gelu_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,  \
-                               void*, void*) {                                                                \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, true, false, nullptr)                                         \
-  }                                                                                                           \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
-      gemm_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,                   \
-                               _Float16* output, int m, int n, int k, void*, void*) {                         \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, false, true, bias)                                            \
-  }                                                                                                           \
-  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                         \
-      gemm_gelu_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,              \
-                                    _Float16* output, int m, int n, int k, void*, void*) {                    \
-    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, true, true, bias)                                             \
+// WK depth groups per stage, SP workgroups per output tile (split-K; the
+// first reserved argument is then the runtime scratch).
+#define CT_DEFINE_GEMM_NT_FULL(NAME, BM, BN, BK, ST, WM, WN, WK, SP)                                         \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                          \
+      gemm_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,        \
+                          void* scratch, void*) {                                                              \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, SP, false, false, nullptr)                                     \
+  }                                                                                                            \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                          \
+      gemm_gelu_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, _Float16* output, int m, int n, int k,   \
+                               void* scratch, void*) {                                                         \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, SP, true, false, nullptr)                                      \
+  }                                                                                                            \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                          \
+      gemm_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,                    \
+                               _Float16* output, int m, int n, int k, void* scratch, void*) {                  \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, SP, false, true, bias)                                         \
+  }                                                                                                            \
+  CT_KERNEL void __launch_bounds__(64 * WM * WN * WK)                                                          \
+      gemm_gelu_bias_nt_fp16_##NAME(const _Float16* a, const _Float16* bt, const _Float16* bias,               \
+                                    _Float16* output, int m, int n, int k, void* scratch, void*) {             \
+    CT_GEMM_NT_BODY(BM, BN, BK, ST, WM, WN, WK, SP, true, true, bias)                                          \
   }
 
+#define CT_DEFINE_GEMM_NT_GROUPS(NAME, BM, BN, BK, ST, WM, WN, WK) \
+  CT_DEFINE_GEMM_NT_FULL(NAME, BM, BN, BK, ST, WM, WN, WK, 1)
 #define CT_DEFINE_GEMM_NT(NAME, BM, BN, BK, ST, WM, WN) CT_DEFINE_GEMM_NT_GROUPS(NAME, BM, BN, BK, ST, WM, WN, 1)
+#define CT_DEFINE_GEMM_NT_SPLIT(NAME, BM, BN, BK, ST, WM, WN, SP) \
+  CT_DEFINE_GEMM_NT_FULL(NAME, BM, BN, BK, ST, WM, WN, 1, SP)
 
 // name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N
 CT_DEFINE_GEMM_NT(m256n256w4, 256, 256, 64, 2, 2, 2)
@@ -472,3 +555,8 @@ CT_DEFINE_GEMM_NT(m128n128k128w8, 128, 128, 128, 2, 2, 4)
 CT_DEFINE_GEMM_NT(m128n64w8, 128, 64, 64, 2, 4, 2)
 // name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N, depth groups
 CT_DEFINE_GEMM_NT_GROUPS(m128n128k128w2x2k2, 128, 128, 128, 2, 2, 2, 2)
+// name, BLOCK_M, BLOCK_N, BLOCK_K, stages, wavefronts along M, along N, workgroups per tile
+CT_DEFINE_GEMM_NT_SPLIT(m64n64s2, 64, 64, 64, 2, 2, 2, 2)
+CT_DEFINE_GEMM_NT_SPLIT(m64n64s4, 64, 64, 64, 2, 2, 2, 4)
+CT_DEFINE_GEMM_NT_SPLIT(m128n64s4, 128, 64, 64, 2, 4, 2, 4)
+CT_DEFINE_GEMM_NT_SPLIT(m128n128s2, 128, 128, 64, 2, 2, 4, 2)

@@ -20,7 +20,7 @@ from pathlib import Path
 import pytest
 
 from cutriton_amd import engine, native, workloads
-from cutriton_amd.kernel_specs.transformer import GEMM_NT_TILES
+from cutriton_amd.kernel_specs.transformer import GEMM_NT_SPLIT_TILES, GEMM_NT_TILES
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -109,8 +109,9 @@ def test_ffn_plan_and_candidates(gfx950):
     assert [op.op_type for op in ops] == ["GemmGelu", "Gemm", "SkipLayerNormalization"]
     for op in ops:
         assert sum(c.startswith("unfused:") for c in op.candidates) == (0 if op.op_type == "Gemm" else 1)
-    # every weight-transposed tile, four B-as-is tiles, then Gemm,Gelu
-    assert len(ops[0].candidates) == len(GEMM_NT_TILES) + 5
+    # every weight-transposed tile (whole depth and split-K), four B-as-is
+    # tiles, then Gemm,Gelu
+    assert len(ops[0].candidates) == len(GEMM_NT_TILES) + len(GEMM_NT_SPLIT_TILES) + 5
     assert ops[0].candidates[ops[0].selected_candidate].endswith("gemm_gelu_bias.fp16.mfma:m128n128w4")
     assert ops[0].candidates[-1] == "unfused:gemm_gelu"
 

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from cutriton_amd import engine, workloads
-from cutriton_amd.kernel_specs.transformer import ROW_VARIANTS
+from cutriton_amd.kernel_specs.transformer import GEMM_NT_SPLIT_TILES, GEMM_NT_TILES, ROW_VARIANTS
 from oracle import oracle
 from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant, only_variant, run_graph,
                            without_kernels)
@@ -28,9 +28,7 @@ CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64"
                  "direct:d64n256", "direct:d64n64", "direct:d32n64")
 # (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
 # "_kn" reads B as it is.
-GEMM16_VARIANTS = tuple(("", v) for v in ("m256n256w4", "m256n256w8", "m256n128w4", "m128n256w4", "m128n128w4",
-                                          "m128n128k128w4", "m64n128w4", "m64n64w4", "m256n128w8", "m128n256w8",
-                                          "m128n128w8", "m128n128k128w8", "m128n64w8")) + \
+GEMM16_VARIANTS = tuple(("", v[0]) for v in GEMM_NT_TILES + GEMM_NT_SPLIT_TILES) + \
     tuple(("_kn", v) for v in ("m64n64k64", "m128n128k64", "m256n128k64", "m256n256k64"))
 
 
@@ -389,6 +387,37 @@ def test_gemm_fp16_variants(tmp_path, family, variant, gelu, bias):
         want = oracle.evaluate(g, feeds)[g.outputs[0]]
         err = np.abs(out[g.outputs[0]].astype(np.float64) - want)
         assert err.max() <= 1e-2, f"{kid}:{variant} {(m, k, n)} max abs err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("variant", [v[0] for v in GEMM_NT_SPLIT_TILES])
+def test_gemm_fp16_split_k_shares_follow_the_inputs(tmp_path, variant):
+    """FP16 split-K: consecutive launches on one context with different
+    inputs each match the oracle (a stale share or counter from the previous
+    launch would not), also under hipGraph replay; the last share of the
+    (1, 8, 4) product is empty (one depth tile for up to four shares)."""
+    import torch
+
+    rng = np.random.default_rng(29)
+    kid = "gemm_gelu_bias.fp16.mfma"
+    pack = filtered_pack(tmp_path / "pack", lambda e: e["kernel_id"] not in (kid, kid + "_kn") or
+                         (e["kernel_id"] == kid and e["variant_id"] == variant))
+    for m, k, n in ((512, 3072, 768), (1, 8, 4)):
+        g, feeds_a = gemm16_graph(rng, m, k, n, True, True)
+        feeds_b = {"a": (rng.standard_normal((m, k)) * 2).astype(np.float16)}
+        eng = engine.build_engine(workloads.to_model(g), engine.CompileOptions(kernel_artifact_dir=pack,
+                                                                               tuning_mode="disabled"))
+        assert eng.ops()[0].candidates[eng.ops()[0].selected_candidate].endswith(f"{kid}:{variant}")
+        ctx = eng.create_execution_context()
+        a = torch.empty((m, k), dtype=torch.float16, device="cuda:0")
+        y = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+        ctx.bind_input("a", a, layout="")
+        ctx.bind_output(g.outputs[0], y, layout="")
+        want = {"a": oracle.evaluate(g, feeds_a)[g.outputs[0]], "b": oracle.evaluate(g, feeds_b)[g.outputs[0]]}
+        for which in ("a", "b", "b", "a", "b"):
+            a.copy_(torch.from_numpy((feeds_a if which == "a" else feeds_b)["a"]))
+            ctx.run()
+            err = np.abs(y.cpu().numpy().astype(np.float64) - want[which]).max()
+            assert err <= 1e-2, f"{variant} {(m, k, n)} input {which}: max abs err {err:.3e}"
 
 
 @pytest.mark.parametrize("family", ["", "_kn"])
