@@ -53,6 +53,7 @@ import tempfile
 import time
 from collections import defaultdict
 from pathlib import Path
+from typing import Any, NamedTuple
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -109,21 +110,34 @@ def _context(graph, feeds, cache_dir: str, profiling: bool, tuning_mode: str, pr
     return eng, ctx, (inputs, outputs)
 
 
-def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles=None):
+class Run(NamedTuple):
+    ms_per_step: float          # wall time per step over the timed steps
+    median_event_ms: float      # median of per-step HIP event pairs
+    kernel_ms: list[float]      # per op: TimeOp kernel duration
+    graph_event_ms: list[float]  # per op: profiled-graph event duration per step
+    ops: list[Any]
+    selected: list[str]         # per op: the tuned candidate
+
+
+def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles=None) -> Run:
     """Tunes `graph` (TuneOnMiss), then:
       1. a profiled engine replays `steps` steps and sums each op's HIP-event
          duration (kernel time, read from the event nodes inside the graph);
       2. an unprofiled engine built from the tuning cache (UseCache) replays
          `steps` steps bracketed by device synchronisation: the wall time of
          these is the step time.
-      3. each op's selected kernels are timed over back-to-back launches on
-         the measured stream (ExecutionContext::TimeOp).
-    Returns (ms per step, per-op kernel ms, per-op graph-event ms per step,
-    plan ops, selected candidate per op)."""
+      3. the same engine's steps are timed again one by one between HIP
+         events on that stream (the reference harness's figure), median kept;
+      4. each op's selected kernels are timed over back-to-back launches on
+         the measured stream (ExecutionContext::TimeOp)."""
     import torch
 
-    stream = torch.cuda.current_stream()
+    # A stream of the caller's own (default priority), as the reference
+    # harness creates one: RunAsync enqueues the graph on it, so events
+    # recorded on it bracket the step.
+    stream = torch.cuda.Stream()
     handle = stream.cuda_stream
+    torch.cuda.synchronize()
     eng, ctx, keep = _context(graph, feeds, cache_dir, True, "tune_on_miss", profiles)
     t0 = time.perf_counter()
     ctx.run_async(handle)  # first run: tuning, module loads, graph capture
@@ -158,11 +172,22 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles
         ctx.synchronize()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - wall0) * 1e3 / steps
+    # The reference harness's figure: event pair around each RunAsync,
+    # median over the steps (resnet50_native.cpp:281-291).
+    latencies = []
+    for _ in range(steps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        ctx.run_async(handle)
+        end.record(stream)
+        ctx.synchronize()
+        latencies.append(start.elapsed_time(end))
+    median_ms = sorted(latencies)[len(latencies) // 2]
     # Kernel time per op on the same stream: back-to-back launches between
     # one event pair, free of the event nodes' dispatch gaps.
     kernel_ms = [ctx.time_op(i, KERNEL_TIMING_LAUNCHES, handle) for i in range(len(ops))]
     graph_event_ms = [v / steps for v in op_ms]
-    return ms_per_step, kernel_ms, graph_event_ms, ops, selected
+    return Run(ms_per_step, median_ms, kernel_ms, graph_event_ms, ops, selected)
 
 
 # --- algorithmic work --------------------------------------------------------
@@ -206,8 +231,9 @@ def bench_resnet(args, cache_dir: str, batch: int, profile: bool) -> dict:
 
     graph = workloads.resnet50(1 if profile else batch)
     x = workloads.resnet50_input(batch)
-    ms_per_step, kernel_ms, event_ms, ops, selected = run_workload(
-        graph, {"input": x}, args.steps, args.warmup, cache_dir, RESNET_PROFILE if profile else None)
+    run = run_workload(graph, {"input": x}, args.steps, args.warmup, cache_dir, RESNET_PROFILE if profile else None)
+    ms_per_step, kernel_ms, event_ms, ops, selected = (run.ms_per_step, run.kernel_ms, run.graph_event_ms, run.ops,
+                                                       run.selected)
     # The profile engine's graph is declared at batch 1; FLOPs and bytes
     # are those of the batch it runs.
     at_batch = dataclasses.replace(graph, inputs={"input": ((batch, 3, 224, 224), "float32", "NCHW")})
@@ -238,6 +264,7 @@ def bench_resnet(args, cache_dir: str, batch: int, profile: bool) -> dict:
     return {
         "engine": engine_kind,
         "ms_per_step": ms_per_step,
+        "median_event_ms": run.median_event_ms,
         "img_s": img_s,
         "tflops": total_flops / (ms_per_step * 1e-3) / 1e12,
         "pct_fp32_mfma_peak": 100.0 * total_flops / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
@@ -266,7 +293,8 @@ def bench_single_node(args, cache_dir: str) -> dict:
     from cutriton_amd import workloads
 
     graph, x = workloads.conv_bn_relu()
-    ms_per_step, kernel_ms, _, ops, selected = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir)
+    run = run_workload(graph, {"x": x}, args.steps, args.warmup, cache_dir)
+    ms_per_step, kernel_ms, selected = run.ms_per_step, run.kernel_ms, run.selected
     flops = sum(workloads.node_flops(graph).values())
     out = {
         "workload": "conv_bn_relu_fp32_1x64x56x56_k3s1p1",
@@ -289,8 +317,8 @@ def bench_ffn(args, cache_dir: str, shape: tuple[int, int, int], profile: bool) 
         x = x[:m]
     else:
         template, x = workloads.ffn(m, h, i)
-    ms_per_step, kernel_ms, _, ops, selected = run_workload(template, {"x": x}, args.steps, args.warmup, cache_dir,
-                                                            FFN_PROFILE if profile else None)
+    run = run_workload(template, {"x": x}, args.steps, args.warmup, cache_dir, FFN_PROFILE if profile else None)
+    ms_per_step, kernel_ms, ops, selected = run.ms_per_step, run.kernel_ms, run.ops, run.selected
     gemm_flops = 2 * m * h * i
     per_op = {op.op_type: kernel_ms[j] for j, op in enumerate(ops)}
     gemm_ms = per_op["GemmGelu"] + per_op["Gemm"]
@@ -300,6 +328,7 @@ def bench_ffn(args, cache_dir: str, shape: tuple[int, int, int], profile: bool) 
         "workload": f"ffn_fp16_m{m}_h{h}_i{i}",
         "engine": "profile min128/opt4096/max8192" if profile else "static",
         "ms_per_step": ms_per_step,
+        "median_event_ms": run.median_event_ms,
         "tflops_block": 2 * gemm_flops / (ms_per_step * 1e-3) / 1e12,
         "gemm_gelu_us": per_op["GemmGelu"] * 1e3,
         "gemm_us": per_op["Gemm"] * 1e3,
@@ -348,7 +377,8 @@ def bench_norms(args, cache_dir: str) -> dict:
     g.inputs["x"] = ((rows, columns), "float16", "")
     g.add("softmax", "Softmax", ["x"], ["y"], axis=-1)
     g.outputs.append("y")
-    _, kernel_ms, _, _, selected = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    run = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    kernel_ms, selected = run.kernel_ms, run.selected
     out.update(softmax_us=kernel_ms[0] * 1e3, softmax_gbps=moved / (kernel_ms[0] * 1e-3) / 1e9,
                softmax_variant=selected[0].rsplit(":", 1)[1])
     g = workloads.GraphSpec()
@@ -357,7 +387,7 @@ def bench_norms(args, cache_dir: str) -> dict:
     beta = g.constant("beta", rng.normal(0.0, 0.1, columns).astype(np.float16))
     g.add("ln", "LayerNormalization", ["x", gamma, beta], ["y"], axis=-1, epsilon=1e-5)
     g.outputs.append("y")
-    _, kernel_ms, _, _, _ = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    kernel_ms = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir).kernel_ms
     out.update(layer_norm_us=kernel_ms[0] * 1e3, layer_norm_gbps=(moved + 4 * columns) / (kernel_ms[0] * 1e-3) / 1e9)
     log(f"  softmax: {out['softmax_us']:.1f} us ({out['softmax_gbps']:.0f} GB/s, {out['softmax_variant']}); "
         f"layer norm: {out['layer_norm_us']:.1f} us ({out['layer_norm_gbps']:.0f} GB/s)")
@@ -383,7 +413,7 @@ def bench_attention(args, cache_dir: str) -> dict:
             g.inputs[n] = ((b, h, s, d), "float16", "")
         g.add("attention", "Attention", ["q", "k", "v"], ["o"], is_causal=int(causal))
         g.outputs.append("o")
-        _, kernel_ms, _, _, _ = run_workload(g, feeds, args.steps, args.warmup, cache_dir)
+        kernel_ms = run_workload(g, feeds, args.steps, args.warmup, cache_dir).kernel_ms
         pairs = s * (s + 1) // 2 if causal else s * s
         flops = 4 * b * h * pairs * d
         key = "causal" if causal else "full"
@@ -413,8 +443,8 @@ def bench_copy(args, cache_dir: str) -> dict:
     """The Relu copy's GB/s: the streaming reference for the bandwidth
     kernels."""
     g, x = copy_graph()
-    ms_per_step, op_kernel_ms, _, ops, _ = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
-    kernel_ms = op_kernel_ms[0]
+    run = run_workload(g, {"x": x}, args.steps, args.warmup, cache_dir)
+    ms_per_step, kernel_ms = run.ms_per_step, run.kernel_ms[0]
     out = {"workload": "relu_fp32_64Mi", "bytes": 2 * 4 * COPY_FLOATS, "kernel_us": kernel_ms * 1e3,
            "gbps": 2 * 4 * COPY_FLOATS / (kernel_ms * 1e-3) / 1e9, "ms_per_step": ms_per_step}
     log(f"  copy: {out['kernel_us']:.1f} us, {out['gbps']:.0f} GB/s")
@@ -621,6 +651,7 @@ def main() -> int:
     if args.workload in ("all", "resnet50", "resnet50_bs32"):
         r = bench_resnet(args, cache_dir, 32, profile=True)
         result.update(value=round(r["img_s"], 2), ms_per_step=round(r["ms_per_step"], 4),
+                      median_event_ms=round(r["median_event_ms"], 4),
                       pct_fp32_mfma_peak=round(r["pct_fp32_mfma_peak"], 2), roofline=r["roofline"])
         result["resnet50_tflops"] = round(r["tflops"], 3)
     if args.workload in ("all", "resnet50"):
