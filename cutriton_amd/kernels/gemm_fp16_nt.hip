@@ -17,10 +17,12 @@
 // reordering.
 //
 // Pipeline. A workgroup owns a BM x BN output tile and walks the depth in
-// BK-deep tiles through a ring of STAGES LDS stages. The loads of tile
-// kt + STAGES - 1 are issued (straight into LDS, with buffer_load ... lds)
-// before tile kt is multiplied, so STAGES - 1 tiles are in flight behind the
-// MFMAs. One barrier per depth tile orders reuse of a stage.
+// BK-deep tiles through a ring of STAGES LDS stages, with STAGES - 1 tiles
+// in flight (straight into LDS, with buffer_load ... lds) behind the MFMAs.
+// One barrier per depth tile orders reuse of a stage; it sits in the middle
+// of the tile's last MFMA step, so that the next tile's first fragment
+// reads and the barrier wait overlap matrix work (measured 5% faster on the
+// 4096 x 4096 x 1024 GemmGelu than a barrier between tiles).
 //
 // LDS layout. A stage holds BM A rows then BN B rows of BK halves, i.e.
 // CH = BK / 8 chunks of 16 bytes per row. Chunk c of row r sits at chunk
@@ -168,7 +170,7 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   static_assert(STAGES >= 2 && STAGES <= 4, "ring of 2..4 stages");
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 16x16 MFMA tile");
   static_assert(LOADS * RPL * WAVES == BM + BN && BM % RPL == 0, "loads split evenly; none straddles A and B");
-  static_assert(2 * LOADS < 64, "vmcnt range");
+  static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
   static_assert(SPLIT == 1 || WAVES_K == 1, "split-K keeps each stage's depth in one workgroup");
 
   const int tid = threadIdx.x;
@@ -241,61 +243,13 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   const int b_row = (BM + wn + lane16) * CH;
   const int swz = (lane16 / (16 / CH)) % CH;
 
-  // MFMAs of one stage. The fragments of step s + 1 are read while the
-  // MFMAs of step s run; the scheduling groups at the end fix the order of
-  // the whole stage (first reads, then per step one LDS read after each of
-  // the first TM + TN MFMAs), so the read latency hides behind the matrix
-  // pipeline instead of stalling it.
-  auto compute_tile = [&](int stage) {
-    const u32x4* tile_base = lds + stage * S::kStageChunks;
-    const int first_step = wk * GROUP_STEPS;
-    f16x8 af[2][TM];
-    f16x8 bf[2][TN];
-    auto read_frags = [&](int step, f16x8* fa, f16x8* fb) {
-      const int chunk = (4 * (first_step + step) + quarter) ^ swz;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = __builtin_bit_cast(f16x8, tile_base[a_row + i * 16 * CH + chunk]);
-#pragma unroll
-      for (int t = 0; t < TN; ++t) fb[t] = __builtin_bit_cast(f16x8, tile_base[b_row + t * 16 * CH + chunk]);
-    };
-    read_frags(0, af[0], bf[0]);
-#pragma unroll
-    for (int step = 0; step < GROUP_STEPS; ++step) {
-      const int cur_f = step & 1;
-      if (step + 1 < GROUP_STEPS) read_frags(step + 1, af[cur_f ^ 1], bf[cur_f ^ 1]);
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[cur_f][t], af[cur_f][i], acc[t][i], 0, 0, 0);
-    }
-    constexpr int READS = TM + TN;
-    constexpr int MFMAS = TM * TN;
-    constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS, 0);
-#pragma unroll
-    for (int step = 0; step < GROUP_STEPS; ++step) {
-      if (step + 1 < GROUP_STEPS) {
-#pragma unroll
-        for (int q = 0; q < PAIRS; ++q) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        }
-        if (READS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - PAIRS, 0);
-        if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
-      } else {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS, 0);
-      }
-    }
-  };
-
   // Waits until this wavefront's loads of tile kt have landed, `later` being
   // the number of tiles issued after it (LOADS instructions each).
   auto wait_tile = [&](int later) {
     if (!VEC) return;  // the element-wise path stored synchronously
-    if (later >= 2) {
-      WaitVmcnt<2 * LOADS>();
-    } else if (later == 1) {
+    if (STAGES >= 4 && later >= 2) {
+      WaitVmcnt<(STAGES >= 4 ? 2 : 0) * LOADS>();
+    } else if (later >= 1) {
       WaitVmcnt<LOADS>();
     } else {
       WaitVmcnt<0>();
@@ -313,16 +267,104 @@ __device__ __forceinline__ void GemmNtCore(u32x4* __restrict__ lds, const _Float
   const int kb = min(k_tiles_all, split * per_split);
   const int ke = min(k_tiles_all, kb + per_split);
   const int k_tiles = ke - kb;
+
+  // Fragments, double-buffered by MFMA step: a lane's 8 depths of one row
+  // of A (af) or of B (bf) per 16-row block.
+  const int first_step = wk * GROUP_STEPS;
+  f16x8 af[2][TM];
+  f16x8 bf[2][TN];
+  auto read_frags = [&](int stage, int step, f16x8* fa, f16x8* fb) {
+    const u32x4* tile_base = lds + stage * S::kStageChunks;
+    const int chunk = (4 * (first_step + step) + quarter) ^ swz;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = __builtin_bit_cast(f16x8, tile_base[a_row + i * 16 * CH + chunk]);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) fb[t] = __builtin_bit_cast(f16x8, tile_base[b_row + t * 16 * CH + chunk]);
+  };
+  // MFMAs [from, to) of one step, t-major.
+  auto mfmas = [&](const f16x8* fa, const f16x8* fb, int from, int to) {
+#pragma unroll
+    for (int q = from; q < to; ++q)
+      acc[q / TM][q % TM] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[q / TM], fa[q % TM], acc[q / TM][q % TM], 0, 0, 0);
+  };
+  constexpr int READS = TM + TN;
+  constexpr int MFMAS = TM * TN;
+  constexpr int HALF = MFMAS / 2;  // MFMAs of a stage's last step issued before its barrier
+  constexpr int TAIL = MFMAS - HALF;
+  constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
+  constexpr int TAIL_PAIRS = READS < TAIL ? READS : TAIL;
+
+  // Pipeline. Depth tile kt + 1 is ordered after tile kt by one barrier,
+  // placed in the middle of tile kt's last MFMA step: the first HALF of that
+  // step's MFMAs are issued, then this wavefront waits for its loads of tile
+  // kt + 1, meets the others at the barrier (after which every load of tile
+  // kt + 1 has landed and no wavefront reads tile kt's stage any more: the
+  // last step's fragments are in registers), issues the loads of tile
+  // kt + STAGES into that stage, and reads the first fragments of tile
+  // kt + 1 while the other TAIL MFMAs run. The barrier wait and the first
+  // read latency of each stage thus hide behind matrix work. Within a stage,
+  // the fragments of step s + 1 are read while the MFMAs of step s run; the
+  // scheduling groups fix that order (one LDS read after each MFMA).
+  //
+  // P is the fragment buffer of the stage's first step: with an odd number
+  // of steps per stage it alternates from stage to stage.
+  auto run_stage = [&](auto p_const, int kt) {
+    constexpr int P = decltype(p_const)::value;
+    const int stage = kt % STAGES;
+#pragma unroll
+    for (int step = 0; step + 1 < GROUP_STEPS; ++step) {
+      const int cur = (P + step) & 1;
+      read_frags(stage, step + 1, af[cur ^ 1], bf[cur ^ 1]);
+      mfmas(af[cur], bf[cur], 0, MFMAS);
+#pragma unroll
+      for (int q = 0; q < PAIRS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      if (READS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - PAIRS, 0);
+      if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    constexpr int LAST = (P + GROUP_STEPS - 1) & 1;
+    mfmas(af[LAST], bf[LAST], 0, HALF);
+    __builtin_amdgcn_sched_barrier(0);
+    // After the last stage the wait, the barrier and the fragment reads
+    // (of a stage that holds no further tile) are idle work, kept so that
+    // the stage stays one straight block of register code.
+    wait_tile(min(STAGES - 2, k_tiles - 2 - kt));
+    __syncthreads();
+    if (kt + STAGES < k_tiles) load_tile(stage, kb + kt + STAGES);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags((kt + 1) % STAGES, 0, af[LAST ^ 1], bf[LAST ^ 1]);
+    mfmas(af[LAST], bf[LAST], HALF, MFMAS);
+#pragma unroll
+    for (int q = 0; q < TAIL_PAIRS; ++q) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    if (READS > TAIL_PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - TAIL_PAIRS, 0);
+    if (TAIL > TAIL_PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, TAIL - TAIL_PAIRS, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: tiles 0 .. STAGES - 2 in flight, tile 0 landed everywhere,
+  // tile STAGES - 1 issued, the first fragments read.
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < k_tiles) load_tile(s, kb + s);
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    wait_tile(min(STAGES - 2, k_tiles - 1 - kt));
-    // After the barrier every wavefront's loads of tile kt have landed and
-    // every wavefront is done with tile kt - 1, whose stage takes the next load.
+  if (k_tiles > 0) {
+    wait_tile(min(STAGES - 2, k_tiles - 1));
     __syncthreads();
-    if (kt + STAGES - 1 < k_tiles) load_tile((kt + STAGES - 1) % STAGES, kb + kt + STAGES - 1);
-    compute_tile(kt % STAGES);
+    if (STAGES - 1 < k_tiles) load_tile(STAGES - 1, kb + STAGES - 1);
+    read_frags(0, 0, af[0], bf[0]);
+  }
+  if constexpr (GROUP_STEPS % 2 == 0) {
+    for (int kt = 0; kt < k_tiles; ++kt) run_stage(std::integral_constant<int, 0>(), kt);
+  } else {
+    for (int kt = 0; kt < k_tiles; kt += 2) {
+      run_stage(std::integral_constant<int, 0>(), kt);
+      if (kt + 1 < k_tiles) run_stage(std::integral_constant<int, 1>(), kt + 1);
+    }
   }
 
   if (SPLIT > 1 && split_fits) {
