@@ -100,26 +100,28 @@ __device__ __forceinline__ u32x4 LoadChunkScalar(const _Float16* base, int row, 
 // erfc follows Abramowitz & Stegun, Handbook of Mathematical Functions,
 // formula 7.1.28: erfc(z) = 1 / (1 + a1 z + ... + a6 z^6)^16 for z >= 0,
 // absolute error at most 3e-7. The polynomial is evaluated in x = z * sqrt 2
-// (coefficients a_i / sqrt(2)^i). For large x the 16th power overflows to
-// +inf and its reciprocal is 0, so GELU(a) = max(a, 0) there. FP32
-// evaluation keeps the total absolute error below 1e-6.
+// with every coefficient (the leading 1 too) scaled by 2^(1/16): its 16th
+// power is then twice A&S's, and its reciprocal is Q itself, with no
+// separate halving. Coefficient i is a_i / sqrt(2)^i * 2^(1/16). For large x
+// the 16th power overflows to +inf and its reciprocal is 0, so GELU(a) =
+// max(a, 0) there. FP32 evaluation keeps the total absolute error below 1e-6.
 __device__ __forceinline__ float GeluErfAs(float a) {
   const float x = __builtin_fabsf(a);
-  float p = 5.3829750e-06f;                   // a6 / sqrt(2)^6
-  p = __builtin_fmaf(p, x, 4.8889953e-05f);   // a5 / sqrt(2)^5
-  p = __builtin_fmaf(p, x, 3.8003575e-05f);   // a4 / sqrt(2)^4
-  p = __builtin_fmaf(p, x, 3.2776560e-03f);   // a3 / sqrt(2)^3
-  p = __builtin_fmaf(p, x, 2.1141006e-02f);   // a2 / sqrt(2)^2
-  p = __builtin_fmaf(p, x, 4.9867346e-02f);   // a1 / sqrt(2)
-  p = __builtin_fmaf(p, x, 1.0f);
+  float p = 5.6212997e-06f;
+  p = __builtin_fmaf(p, x, 5.1055209e-05f);
+  p = __builtin_fmaf(p, x, 3.9686137e-05f);
+  p = __builtin_fmaf(p, x, 3.4227392e-03f);
+  p = __builtin_fmaf(p, x, 2.2076999e-02f);
+  p = __builtin_fmaf(p, x, 5.2075163e-02f);
+  p = __builtin_fmaf(p, x, 1.0442738f);  // 2^(1/16)
   p = p * p;
   p = p * p;
   p = p * p;
   p = p * p;
-  const float q = __builtin_amdgcn_rcpf(p);  // erfc(x / sqrt 2)
+  const float q = __builtin_amdgcn_rcpf(p);  // Q(x)
   // x * Q(x) is below 1e-50 from x = 16 on; the clamp keeps +inf finite there
   // (inf * 0) so that GELU(+inf) = +inf.
-  return __builtin_fmaf(-0.5f * __builtin_fminf(x, 16.0f), q, __builtin_fmaxf(a, 0.0f));
+  return __builtin_fmaf(__builtin_fminf(x, 16.0f), -q, __builtin_fmaxf(a, 0.0f));
 }
 
 template <int BM, int BN, int BK, int STAGES>
