@@ -339,53 +339,35 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   const int quarter = lane >> 4;
   const int lane16 = lane & 15;
 
-  // MFMAs of one LDS depth tile (buffer `cur`) into acc. The fragments of
-  // group g + 1 are read while the MFMAs of group g run; the scheduling
-  // groups at the end fix that order (first reads, then one LDS read after
-  // each of the first TM + TN MFMAs of a group).
-  auto compute_tile = [&](int cur) {
-    const float* at = a_tile + cur * L::kA + (wm + lane16) * ROW + 4 * quarter;
-    const float* bt = b_tile + cur * L::kB + (wn + lane16) * ROW + 4 * quarter;
-    f32x4 av[2][TM];
-    f32x4 bv[2][TN];
-    auto read_frags = [&](int gi, f32x4* fa, f32x4* fb) {
-      const int col = (wk * WAVE_GROUPS + gi) * 16;
+  // Fragments, double-buffered by 16-depth group: a lane's four depths of
+  // one row of A (av) or of B (bv) per 16-row block.
+  f32x4 av[2][TM];
+  f32x4 bv[2][TN];
+  auto read_frags = [&](int buf, int gi, f32x4* fa, f32x4* fb) {
+    const float* at = a_tile + buf * L::kA + (wm + lane16) * ROW + 4 * quarter;
+    const float* bt = b_tile + buf * L::kB + (wn + lane16) * ROW + 4 * quarter;
+    const int col = (wk * WAVE_GROUPS + gi) * 16;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const f32x4*>(at + i * 16 * ROW + col);
+    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const f32x4*>(at + i * 16 * ROW + col);
 #pragma unroll
-      for (int t = 0; t < TN; ++t) fb[t] = *reinterpret_cast<const f32x4*>(bt + t * 16 * ROW + col);
-    };
-    read_frags(0, av[0], bv[0]);
+    for (int t = 0; t < TN; ++t) fb[t] = *reinterpret_cast<const f32x4*>(bt + t * 16 * ROW + col);
+  };
+  // MFMAs [from, to) of one group, in (e, i, t) order.
+  auto mfmas = [&](const f32x4* fa, const f32x4* fb, int from, int to) {
 #pragma unroll
-    for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
-      const int c = gi & 1;
-      if (gi + 1 < WAVE_GROUPS) read_frags(gi + 1, av[c ^ 1], bv[c ^ 1]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int t = 0; t < TN; ++t)
-            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[c][i][e], bv[c][t][e], acc[i][t], 0, 0, 0);
-    }
-    constexpr int READS = TM + TN;
-    constexpr int MFMAS = 4 * TM * TN;
-    constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS, 0);
-#pragma unroll
-    for (int gi = 0; gi < WAVE_GROUPS; ++gi) {
-      if (gi + 1 < WAVE_GROUPS) {
-#pragma unroll
-        for (int q = 0; q < PAIRS; ++q) {
-          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        }
-        if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
-      } else {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS, 0);
-      }
+    for (int q = from; q < to; ++q) {
+      const int e = q / (TM * TN);
+      const int i = (q / TN) % TM;
+      const int t = q % TN;
+      acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][e], fb[t][e], acc[i][t], 0, 0, 0);
     }
   };
+  constexpr int READS = TM + TN;
+  constexpr int MFMAS = 4 * TM * TN;
+  constexpr int HALF = MFMAS / 2;  // MFMAs of a tile's last group issued before its barrier
+  constexpr int TAIL = MFMAS - HALF;
+  constexpr int PAIRS = READS < MFMAS ? READS : MFMAS;
+  constexpr int TAIL_PAIRS = READS < TAIL ? READS : TAIL;
 
   // Residual of the lane's outputs (residual-join epilogue without split-K):
   // loaded before the last depth tile is multiplied, so its latency hides
@@ -424,6 +406,67 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
 
   // Accumulates depth tiles [kb, ke) of the current output tile into acc.
   // Ends with a barrier, after which the LDS tiles are free.
+  //
+  // Depth tile kt + 1 is ordered after tile kt by one barrier in the middle
+  // of tile kt's last group of MFMAs: the first HALF of that group's MFMAs
+  // are issued, the staged loads of tile kt + 1 are written to the other
+  // LDS buffer, the barrier makes them visible (no wavefront reads tile
+  // kt's buffer after it: the last group's fragments are in registers), and
+  // the first fragments of tile kt + 1 are read while the other TAIL MFMAs
+  // run, so the barrier wait and the first read latency of each tile hide
+  // behind matrix work. Within a tile, the fragments of group g + 1 are read
+  // while the MFMAs of group g run; the scheduling groups fix that order.
+  //
+  // P is the fragment buffer of the tile's first group (with an odd number
+  // of groups per wavefront it alternates from tile to tile); MORE says
+  // whether another tile follows. The last tile is peeled off the loop: it
+  // loads nothing and prefetches the residual instead, so the loop body
+  // holds no residual registers.
+  auto depth_tile = [&](auto p_const, auto more_const, int kt, int cur) {
+    constexpr int P = decltype(p_const)::value;
+    constexpr bool MORE = decltype(more_const)::value;
+    if (MORE) {
+      load_tile(st0, (kt + 1) * BK);
+    } else {
+      prefetch_residual();
+    }
+#pragma unroll
+    for (int gi = 0; gi + 1 < WAVE_GROUPS; ++gi) {
+      const int c = (P + gi) & 1;
+      read_frags(cur, gi + 1, av[c ^ 1], bv[c ^ 1]);
+      mfmas(av[c], bv[c], 0, MFMAS);
+#pragma unroll
+      for (int q = 0; q < PAIRS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      if (READS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - PAIRS, 0);
+      if (MFMAS > PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, MFMAS - PAIRS, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    constexpr int LAST = (P + WAVE_GROUPS - 1) & 1;
+    mfmas(av[LAST], bv[LAST], 0, HALF);
+    __builtin_amdgcn_sched_barrier(0);
+    if (MORE) store_tile(st0, cur ^ 1);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (MORE) read_frags(cur ^ 1, 0, av[LAST ^ 1], bv[LAST ^ 1]);
+    mfmas(av[LAST], bv[LAST], HALF, MFMAS);
+    if (MORE) {
+#pragma unroll
+      for (int q = 0; q < TAIL_PAIRS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      if (READS > TAIL_PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, READS - TAIL_PAIRS, 0);
+      if (TAIL > TAIL_PAIRS) __builtin_amdgcn_sched_group_barrier(kSchedMfma, TAIL - TAIL_PAIRS, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using More = std::integral_constant<bool, true>;
+  using Last = std::integral_constant<bool, false>;
   auto run_depth = [&](int kb, int ke) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -435,14 +478,23 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     load_tile(st0, kb * BK);
     store_tile(st0, 0);
     __syncthreads();
-    for (int kt = kb; kt < ke; ++kt) {
-      const int cur = (kt - kb) & 1;
-      const bool more = kt + 1 < ke;
-      if (more) load_tile(st0, (kt + 1) * BK);
-      if (!more) prefetch_residual();
-      compute_tile(cur);
-      if (more) store_tile(st0, cur ^ 1);
-      __syncthreads();
+    if (ke <= kb) return;
+    read_frags(0, 0, av[0], bv[0]);
+    if constexpr (WAVE_GROUPS % 2 == 0) {
+      for (int kt = kb; kt + 1 < ke; ++kt) depth_tile(P0(), More(), kt, (kt - kb) & 1);
+      depth_tile(P0(), Last(), ke - 1, (ke - 1 - kb) & 1);
+    } else {
+      int kt = kb;
+      for (; kt + 2 < ke; kt += 2) {
+        depth_tile(P0(), More(), kt, 0);
+        depth_tile(P1(), More(), kt + 1, 1);
+      }
+      if (kt + 1 < ke) {
+        depth_tile(P0(), More(), kt, 0);
+        depth_tile(P1(), Last(), kt + 1, 1);
+      } else {
+        depth_tile(P0(), Last(), kt, 0);
+      }
     }
   };
 
