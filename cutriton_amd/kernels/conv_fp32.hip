@@ -20,7 +20,9 @@
 //
 // Tiling. A workgroup (4 wavefronts) computes a BM x BN output tile and
 // walks the depth in BK-deep tiles, double buffered in LDS with the next
-// tile's global loads in flight during the MFMAs. The wavefronts form a
+// tile's global loads in flight during the MFMAs; the one barrier per tile
+// sits in the middle of its last MFMA group, so the next tile's first
+// fragment reads overlap matrix work. The wavefronts form a
 // WGM x WGN x WGK grid: each owns a (BM/WGM) x (BN/WGN) block of 16x16 MFMA
 // accumulators over 1/WGK of every depth tile; WGK > 1 partial sums are added
 // through LDS before the epilogue. The 16x16x4 form sustains a higher rate on
