@@ -40,6 +40,7 @@ CONV_TILES = (
     ("m128n64k16", 128, 64, 16),
     ("m64n64k64", 64, 64, 64),
     ("m32n128", 32, 128, 32),
+    ("m128n128k16", 128, 128, 16),
 )
 CONV_DEFAULT = "m64n64"
 
@@ -94,6 +95,9 @@ SPLIT_TILES = (
     ("m64n64s5", 64, 64, 32, 5),
     ("m64n64s6", 64, 64, 32, 6),
     ("m64n64k64s2", 64, 64, 64, 2),
+    ("m64n64k16s2", 64, 64, 16, 2),
+    ("m64n64k16s3", 64, 64, 16, 3),
+    ("m64n64k16s5", 64, 64, 16, 5),
 )
 SPLIT_DEFAULT = "m128n128s4"
 SPLIT_SCRATCH_BYTES = 16384 * 4 + (128 << 20)

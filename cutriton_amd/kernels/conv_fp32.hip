@@ -798,6 +798,7 @@ CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m32n128, 32, 128, 32, 1, 4, 1, 1)
+CT_DEFINE_CONV_VARIANTS(m128n128k16, 128, 128, 16, 2, 2, 1, 1)
 
 // Split-K entry points: the first reserved argument is the runtime scratch
 // (kSplitCounterBytes + kSplitShareBytes, zero-initialised by the engine).
@@ -850,6 +851,9 @@ CT_DEFINE_SPLIT_VARIANTS(m64n64s3, 64, 64, 32, 2, 2, 3)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s5, 64, 64, 32, 2, 2, 5)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s6, 64, 64, 32, 2, 2, 6)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one

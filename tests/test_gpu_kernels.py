@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from cutriton_amd import engine, workloads
+from cutriton_amd.kernel_specs.resnet import CONV_TILES, DIRECT_TILES, SPLIT_TILES
 from cutriton_amd.kernel_specs.transformer import GEMM_NT_SPLIT_TILES, GEMM_NT_TILES, ROW_VARIANTS
 from oracle import oracle
 from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant, only_variant, run_graph,
@@ -20,12 +21,9 @@ from tests.helpers import (assert_close_fp32, filtered_pack, only_kernel_variant
 
 pytestmark = pytest.mark.gpu
 
-CONV_VARIANTS = ("mfma:m128n128", "mfma:m64n256", "mfma:m64n128", "mfma:m128n64", "mfma:m64n64",
-                 "mfma:m64n64k16", "mfma:m64n128k16", "mfma:m128n64k16", "mfma:m64n64k64", "mfma:m32n128",
-                 "splitk:m128n128s2", "splitk:m128n128s4", "splitk:m128n128s8",
-                 "splitk:m64n64s2", "splitk:m64n64s4", "splitk:m64n64s3", "splitk:m64n64s5",
-                 "splitk:m64n64s6", "splitk:m64n64k64s2",
-                 "direct:d64n256", "direct:d64n64", "direct:d32n64")
+# Every conv tile the pack builds: LDS-staged, split-K and register-direct.
+CONV_VARIANTS = tuple(f"mfma:{v[0]}" for v in CONV_TILES) + tuple(f"splitk:{v[0]}" for v in SPLIT_TILES) + \
+    tuple(f"direct:{v[0]}" for v in DIRECT_TILES)
 # (kernel-id suffix, variant): "" reads the constant B from its [N][K] copy,
 # "_kn" reads B as it is.
 GEMM16_VARIANTS = tuple(("", v[0]) for v in GEMM_NT_TILES + GEMM_NT_SPLIT_TILES) + \
