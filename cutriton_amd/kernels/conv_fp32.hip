@@ -793,7 +793,7 @@ CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2, 1)
 CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2, 1)
 CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1, 4)
-CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1, 4)
+CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1, 6)
 CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1, 1)
@@ -812,48 +812,48 @@ CT_DEFINE_CONV_VARIANTS(m128n128k16, 128, 128, 16, 2, 2, 1, 1)
     ConvCore<BM, BN, BK, WGM, WGN, 1, EPI, false, SPLIT>(smem, __VA_ARGS__);                    \
   }
 
-#define CT_DEFINE_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT)                                   \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_relu_fp32_##NAME(                                  \
+#define CT_DEFINE_SPLIT_VARIANTS(NAME, BM, BN, BK, WGM, WGN, SPLIT, MIN_GROUPS)                                 \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN, MIN_GROUPS) conv_bn_relu_fp32_##NAME(                                  \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormRelu, x, weight, scale, bias, mean,         \
                       variance, nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                     \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_fp32_##NAME(                                       \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN, MIN_GROUPS) conv_bn_fp32_##NAME(                                       \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, float* output, CT_CONV_DIMS, float epsilon, void* scratch, void*) {         \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNorm, x, weight, scale, bias, mean, variance,   \
                       nullptr, output, CT_CONV_GEOMETRY, epsilon, scratch)                               \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_bn_add_relu_fp32_##NAME(                              \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN, MIN_GROUPS) conv_bn_add_relu_fp32_##NAME(                              \
       const float* x, const float* weight, const float* scale, const float* bias, const float* mean,     \
       const float* variance, const float* residual, float* output, CT_CONV_DIMS, float epsilon,          \
       void* scratch, void*) {                                                                            \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kBatchNormAddRelu, x, weight, scale, bias, mean,      \
                       variance, residual, output, CT_CONV_GEOMETRY, epsilon, scratch)                    \
   }                                                                                                      \
-  CT_KERNEL void __launch_bounds__(64 * WGM * WGN) conv_fp32_##NAME(const float* x, const float* weight,      \
+  CT_KERNEL void __launch_bounds__(64 * WGM * WGN, MIN_GROUPS) conv_fp32_##NAME(const float* x, const float* weight,      \
                                                               float* output, CT_CONV_DIMS, void* scratch, \
                                                               void*) {                                   \
     CT_SPLIT_DISPATCH(BM, BN, BK, WGM, WGN, SPLIT, kPlain, x, weight, nullptr, nullptr, nullptr, nullptr, \
                       nullptr, output, CT_CONV_GEOMETRY, 0.0f, scratch)                                  \
   }
 
-// name, BM, BN, BK, WGM, WGN, SPLIT
-CT_DEFINE_SPLIT_VARIANTS(m128n128s2, 128, 128, 32, 2, 2, 2)
-CT_DEFINE_SPLIT_VARIANTS(m128n128s4, 128, 128, 32, 2, 2, 4)
-CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8)
-CT_DEFINE_SPLIT_VARIANTS(m64n64s2, 64, 64, 32, 2, 2, 2)
-CT_DEFINE_SPLIT_VARIANTS(m64n64s4, 64, 64, 32, 2, 2, 4)
+// name, BM, BN, BK, WGM, WGN, SPLIT, workgroups per CU the registers must allow
+CT_DEFINE_SPLIT_VARIANTS(m128n128s2, 128, 128, 32, 2, 2, 2, 1)
+CT_DEFINE_SPLIT_VARIANTS(m128n128s4, 128, 128, 32, 2, 2, 4, 1)
+CT_DEFINE_SPLIT_VARIANTS(m128n128s8, 128, 128, 32, 2, 2, 8, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s2, 64, 64, 32, 2, 2, 2, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s4, 64, 64, 32, 2, 2, 4, 1)
 // Split counts that are not powers of two fill the last round of
 // workgroups better for some tile counts (e.g. 200 tiles x 5 = 1000).
-CT_DEFINE_SPLIT_VARIANTS(m64n64s3, 64, 64, 32, 2, 2, 3)
-CT_DEFINE_SPLIT_VARIANTS(m64n64s5, 64, 64, 32, 2, 2, 5)
-CT_DEFINE_SPLIT_VARIANTS(m64n64s6, 64, 64, 32, 2, 2, 6)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s3, 64, 64, 32, 2, 2, 3, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s5, 64, 64, 32, 2, 2, 5, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64s6, 64, 64, 32, 2, 2, 6, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2, 1)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2, 6)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3, 6)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5, 6)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one
