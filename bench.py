@@ -358,6 +358,61 @@ def bench_ffn(args, cache_dir: str, shape: tuple[int, int, int], profile: bool) 
     return out
 
 
+def vendor_ffn_gemms(m: int, h: int, i: int) -> dict:
+    """The FFN's two products through torch on the same GPU (hipBLASLt), as a
+    library reference beside the block's own kernels: X[m,h] @ W1[h,i] + b1,
+    the erf GELU as a kernel of its own, and H[m,i] @ W2[i,h] + b2, FP16
+    with FP32 accumulation. Each is timed over 50 back-to-back calls between
+    events on the current stream, after 10 warm-up calls."""
+    import torch
+
+    gen = torch.Generator().manual_seed(0)
+    dev = "cuda:0"
+    x = torch.randn(m, h, generator=gen).half().to(dev)
+    w1 = (torch.randn(h, i, generator=gen) * 0.02).half().to(dev)
+    w2 = (torch.randn(i, h, generator=gen) * 0.02).half().to(dev)
+    b1 = torch.zeros(i, dtype=torch.float16, device=dev)
+    b2 = torch.zeros(h, dtype=torch.float16, device=dev)
+    # The weights also as [N][K] (the layout of torch.nn.Linear and of this
+    # block's own kernels): F.linear multiplies by their transpose.
+    w1t, w2t = w1.t().contiguous(), w2.t().contiguous()
+    mid = torch.addmm(b1, x, w1)
+    linear = torch.nn.functional.linear
+
+    def per_call_us(fn) -> float:
+        for _ in range(10):
+            fn()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(50):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e3 / 50
+
+    out = {
+        "gemm_bias_h_to_i_us": per_call_us(lambda: torch.addmm(b1, x, w1)),
+        "gemm_bias_h_to_i_nk_us": per_call_us(lambda: linear(x, w1t, b1)),
+        "gelu_us": per_call_us(lambda: torch.nn.functional.gelu(mid)),
+        "gemm_bias_i_to_h_us": per_call_us(lambda: torch.addmm(b2, mid, w2)),
+        "gemm_bias_i_to_h_nk_us": per_call_us(lambda: linear(mid, w2t, b2)),
+        "gemm_h_to_i_us": per_call_us(lambda: torch.matmul(x, w1)),
+        "gemm_h_to_i_nk_us": per_call_us(lambda: linear(x, w1t)),
+        "gemm_i_to_h_us": per_call_us(lambda: torch.matmul(mid, w2)),
+        "gemm_i_to_h_nk_us": per_call_us(lambda: linear(mid, w2t)),
+    }
+    out = {k: round(v, 2) for k, v in out.items()}
+    out["timing"] = ("torch.addmm / torch.matmul ([K][N] weight), torch.nn.functional.linear ([N][K] weight, "
+                     "_nk), torch.nn.functional.gelu; 50 calls between events")
+    log(f"  torch (hipBLASLt) M={m} H={h} I={i}: GEMM+bias {out['gemm_bias_h_to_i_us']:.1f} / "
+        f"{out['gemm_bias_h_to_i_nk_us']:.1f} us ([K][N] / [N][K] weight) + GELU {out['gelu_us']:.1f} us; "
+        f"GEMM+bias {out['gemm_bias_i_to_h_us']:.1f} / {out['gemm_bias_i_to_h_nk_us']:.1f} us; no bias "
+        f"{out['gemm_h_to_i_us']:.1f} / {out['gemm_h_to_i_nk_us']:.1f} and {out['gemm_i_to_h_us']:.1f} / "
+        f"{out['gemm_i_to_h_nk_us']:.1f} us")
+    return out
+
+
 def bench_norms(args, cache_dir: str) -> dict:
     """Softmax over attention scores (16 sequences x 16 heads x 1024 queries,
     1024 keys) and a standalone LayerNorm of the same [262144, 1024] shape,
@@ -669,6 +724,7 @@ def main() -> int:
     if args.workload in ("all", "ffn"):
         f = bench_ffn(args, cache_dir, FFN_SHAPE, profile=True)
         result["ffn"] = _rounded(f)
+        result["ffn"]["torch_hipblaslt"] = vendor_ffn_gemms(*FFN_SHAPE)
         if args.workload == "ffn":
             result.update(value=round(f["tflops_block"], 3), unit="TFLOP/s", ms_per_step=round(f["ms_per_step"], 4),
                           dtype="fp16", config={"workload": f["workload"], "engine": f["engine"],
