@@ -220,7 +220,11 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     f32x4 a[A_CHUNKS];
     float b[B_RUN];
   };
-  Stage st0;
+  // 16-deep tiles keep two tiles' loads in flight (tile kt + 2 is loaded
+  // while tile kt + 1 waits in the other registers for its LDS store): one
+  // such tile is too little MFMA work to cover a load's latency.
+  constexpr bool PREFETCH2 = BK == 16 && WAVE_GROUPS == 1;
+  Stage st[PREFETCH2 ? 2 : 1];
 
   // Channel-run depth order (CHANNEL_RUN, C % BK == 0): depth tile t holds
   // channels [c0, c0 + BK) of one kernel tap (r, s); tiles take c fastest,
@@ -427,8 +431,13 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   auto depth_tile = [&](auto p_const, auto more_const, int kt, int cur) {
     constexpr int P = decltype(p_const)::value;
     constexpr bool MORE = decltype(more_const)::value;
+    // PREFETCH2 (one group per tile, so P is the tile's parity): tile kt + 1
+    // is in st[P ^ 1], tile kt + 2 goes to st[P] (stored one tile ago). A
+    // load past the last tile reads zeros or data that is never stored.
+    constexpr int LOAD = PREFETCH2 ? P : 0;
+    constexpr int STORE = PREFETCH2 ? P ^ 1 : 0;
     if (MORE) {
-      load_tile(st0, (kt + 1) * BK);
+      load_tile(st[LOAD], (kt + (PREFETCH2 ? 2 : 1)) * BK);
     } else {
       prefetch_residual();
     }
@@ -449,7 +458,7 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     constexpr int LAST = (P + WAVE_GROUPS - 1) & 1;
     mfmas(av[LAST], bv[LAST], 0, HALF);
     __builtin_amdgcn_sched_barrier(0);
-    if (MORE) store_tile(st0, cur ^ 1);
+    if (MORE) store_tile(st[STORE], cur ^ 1);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     if (MORE) read_frags(cur ^ 1, 0, av[LAST ^ 1], bv[LAST ^ 1]);
@@ -477,8 +486,9 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][t][r] = 0.0f;
     if (CHANNEL_RUN) seek_run(kb);
-    load_tile(st0, kb * BK);
-    store_tile(st0, 0);
+    load_tile(st[0], kb * BK);
+    store_tile(st[0], 0);
+    if (PREFETCH2) load_tile(st[PREFETCH2 ? 1 : 0], (kb + 1) * BK);
     __syncthreads();
     if (ke <= kb) return;
     read_frags(0, 0, av[0], bv[0]);
@@ -793,7 +803,7 @@ CT_DEFINE_CONV_VARIANTS(m64n256, 64, 256, 16, 1, 4, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m64n128, 64, 128, 32, 1, 2, 2, 1)
 CT_DEFINE_CONV_VARIANTS(m128n64, 128, 64, 32, 2, 1, 2, 1)
 CT_DEFINE_CONV_VARIANTS(m64n64, 64, 64, 32, 2, 2, 1, 4)
-CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1, 6)
+CT_DEFINE_CONV_VARIANTS(m64n64k16, 64, 64, 16, 2, 2, 1, 5)
 CT_DEFINE_CONV_VARIANTS(m64n128k16, 64, 128, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m128n64k16, 128, 64, 16, 2, 2, 1, 1)
 CT_DEFINE_CONV_VARIANTS(m64n64k64, 64, 64, 64, 2, 2, 1, 1)
@@ -851,9 +861,9 @@ CT_DEFINE_SPLIT_VARIANTS(m64n64s3, 64, 64, 32, 2, 2, 3, 1)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s5, 64, 64, 32, 2, 2, 5, 1)
 CT_DEFINE_SPLIT_VARIANTS(m64n64s6, 64, 64, 32, 2, 2, 6, 1)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2, 1)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2, 6)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3, 6)
-CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5, 6)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5, 5)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one
