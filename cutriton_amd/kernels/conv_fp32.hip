@@ -220,10 +220,11 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     f32x4 a[A_CHUNKS];
     float b[B_RUN];
   };
-  // 16-deep tiles keep two tiles' loads in flight (tile kt + 2 is loaded
-  // while tile kt + 1 waits in the other registers for its LDS store): one
-  // such tile is too little MFMA work to cover a load's latency.
-  constexpr bool PREFETCH2 = BK == 16 && WAVE_GROUPS == 1;
+  // Tiles of up to 32 depths keep two tiles' loads in flight (tile kt + 2
+  // is loaded while tile kt + 1 waits in the other registers for its LDS
+  // store): one such tile is too little MFMA work to cover a load's
+  // latency. Only where the second set of staging registers is small.
+  constexpr bool PREFETCH2 = WGK == 1 && BK <= 32 && A_CHUNKS * 4 + B_RUN <= 16;
   Stage st[PREFETCH2 ? 2 : 1];
 
   // Channel-run depth order (CHANNEL_RUN, C % BK == 0): depth tile t holds
@@ -423,19 +424,20 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
   // behind matrix work. Within a tile, the fragments of group g + 1 are read
   // while the MFMAs of group g run; the scheduling groups fix that order.
   //
-  // P is the fragment buffer of the tile's first group (with an odd number
-  // of groups per wavefront it alternates from tile to tile); MORE says
-  // whether another tile follows. The last tile is peeled off the loop: it
+  // Q is the tile's parity; P is the fragment buffer of the tile's first
+  // group (with an odd number of groups per wavefront it alternates from
+  // tile to tile, like Q); MORE says whether another tile follows. The last tile is peeled off the loop: it
   // loads nothing and prefetches the residual instead, so the loop body
   // holds no residual registers.
-  auto depth_tile = [&](auto p_const, auto more_const, int kt, int cur) {
-    constexpr int P = decltype(p_const)::value;
+  auto depth_tile = [&](auto q_const, auto more_const, int kt, int cur) {
+    constexpr int Q = decltype(q_const)::value;  // parity of the tile
+    constexpr int P = WAVE_GROUPS % 2 ? Q : 0;
     constexpr bool MORE = decltype(more_const)::value;
-    // PREFETCH2 (one group per tile, so P is the tile's parity): tile kt + 1
-    // is in st[P ^ 1], tile kt + 2 goes to st[P] (stored one tile ago). A
-    // load past the last tile reads zeros or data that is never stored.
-    constexpr int LOAD = PREFETCH2 ? P : 0;
-    constexpr int STORE = PREFETCH2 ? P ^ 1 : 0;
+    // PREFETCH2: tile kt + 1 is in st[Q ^ 1], tile kt + 2 goes to st[Q]
+    // (stored one tile ago). A load past the last tile reads zeros or data
+    // that is never stored.
+    constexpr int LOAD = PREFETCH2 ? Q : 0;
+    constexpr int STORE = PREFETCH2 ? Q ^ 1 : 0;
     if (MORE) {
       load_tile(st[LOAD], (kt + (PREFETCH2 ? 2 : 1)) * BK);
     } else {
@@ -492,21 +494,18 @@ __device__ __forceinline__ void ConvCore(float* __restrict__ smem, const float* 
     __syncthreads();
     if (ke <= kb) return;
     read_frags(0, 0, av[0], bv[0]);
-    if constexpr (WAVE_GROUPS % 2 == 0) {
-      for (int kt = kb; kt + 1 < ke; ++kt) depth_tile(P0(), More(), kt, (kt - kb) & 1);
-      depth_tile(P0(), Last(), ke - 1, (ke - 1 - kb) & 1);
+    // Tiles go in pairs so that the parity of a tile (its LDS buffer, its
+    // staging registers, its first fragment buffer) is a constant.
+    int kt = kb;
+    for (; kt + 2 < ke; kt += 2) {
+      depth_tile(P0(), More(), kt, 0);
+      depth_tile(P1(), More(), kt + 1, 1);
+    }
+    if (kt + 1 < ke) {
+      depth_tile(P0(), More(), kt, 0);
+      depth_tile(P1(), Last(), kt + 1, 1);
     } else {
-      int kt = kb;
-      for (; kt + 2 < ke; kt += 2) {
-        depth_tile(P0(), More(), kt, 0);
-        depth_tile(P1(), More(), kt + 1, 1);
-      }
-      if (kt + 1 < ke) {
-        depth_tile(P0(), More(), kt, 0);
-        depth_tile(P1(), Last(), kt + 1, 1);
-      } else {
-        depth_tile(P0(), Last(), kt, 0);
-      }
+      depth_tile(P0(), Last(), kt, 0);
     }
   };
 
