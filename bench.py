@@ -119,7 +119,7 @@ class Run(NamedTuple):
     selected: list[str]         # per op: the tuned candidate
 
 
-def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles=None) -> Run:
+def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles=None, warm_ms: float = 0.0) -> Run:
     """Tunes `graph` (TuneOnMiss), then:
       1. a profiled engine replays `steps` steps and sums each op's HIP-event
          duration (kernel time, read from the event nodes inside the graph);
@@ -163,6 +163,13 @@ def run_workload(graph, feeds, steps: int, warmup: int, cache_dir: str, profiles
     if plain != selected:
         raise RuntimeError("the tuning cache did not reproduce the tuned plan")
     for _ in range(warmup):
+        ctx.run_async(handle)
+        ctx.synchronize()
+    # Steps of about 0.1 ms leave the GPU below its steady clocks after a few
+    # warm-up steps (measured: 113 us per FFN step after 5, 105 us after 200),
+    # so a workload may ask for warm-up by time as well.
+    warm0 = time.perf_counter()
+    while (time.perf_counter() - warm0) * 1e3 < warm_ms:
         ctx.run_async(handle)
         ctx.synchronize()
     torch.cuda.synchronize()
@@ -317,7 +324,8 @@ def bench_ffn(args, cache_dir: str, shape: tuple[int, int, int], profile: bool) 
         x = x[:m]
     else:
         template, x = workloads.ffn(m, h, i)
-    run = run_workload(template, {"x": x}, args.steps, args.warmup, cache_dir, FFN_PROFILE if profile else None)
+    run = run_workload(template, {"x": x}, args.steps, args.warmup, cache_dir, FFN_PROFILE if profile else None,
+                       warm_ms=100.0)
     ms_per_step, kernel_ms, ops, selected = run.ms_per_step, run.kernel_ms, run.ops, run.selected
     gemm_flops = 2 * m * h * i
     per_op = {op.op_type: kernel_ms[j] for j, op in enumerate(ops)}
