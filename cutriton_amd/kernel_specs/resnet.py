@@ -98,6 +98,8 @@ SPLIT_TILES = (
     ("m64n64k16s2", 64, 64, 16, 2),
     ("m64n64k16s3", 64, 64, 16, 3),
     ("m64n64k16s5", 64, 64, 16, 5),
+    ("m64n64k16s8", 64, 64, 16, 8),
+    ("m64n64k16s16", 64, 64, 16, 16),
 )
 SPLIT_DEFAULT = "m128n128s4"
 SPLIT_SCRATCH_BYTES = 16384 * 4 + (128 << 20)

@@ -863,6 +863,8 @@ CT_DEFINE_SPLIT_VARIANTS(m64n64k64s2, 64, 64, 64, 2, 2, 2, 1)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k16s2, 64, 64, 16, 2, 2, 2, 5)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k16s3, 64, 64, 16, 2, 2, 3, 5)
 CT_DEFINE_SPLIT_VARIANTS(m64n64k16s5, 64, 64, 16, 2, 2, 5, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s8, 64, 64, 16, 2, 2, 8, 5)
+CT_DEFINE_SPLIT_VARIANTS(m64n64k16s16, 64, 64, 16, 2, 2, 16, 5)
 
 // C[m][n] = sum_k A[m][k] * B[k][n] (+ bias[n]) with A, B row-major: the
 // core with rows = m, columns = n, depth = k (a 1x1 convolution of one

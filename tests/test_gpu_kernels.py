@@ -103,7 +103,7 @@ def test_conv_family_variants(tmp_path, family_variant, tail):
 
 SMALLC_SHAPES = [
     # n, c, h, w, k, r, stride, pad, dil
-    (2, 3, 31, 29, 16, 7, 2, 3, 1),     # stem-like, ragged rows and columns
+    (2, 3, 33, 29, 16, 7, 2, 3, 1),     # stem-like, P = 17 and Q = 15: ragged rows and columns
     (1, 3, 64, 240, 64, 7, 2, 3, 1),    # Q = 120: two column chunks
     (2, 4, 9, 11, 40, 3, 1, 1, 1),      # 3x3, K = 40: a partial channel block
     (1, 1, 12, 12, 8, 1, 1, 0, 1),      # 1x1, one channel
