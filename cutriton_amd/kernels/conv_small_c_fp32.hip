@@ -228,6 +228,48 @@ __device__ __forceinline__ void SmallCConv(const float* __restrict__ x, const fl
   }
 
   // ---- Epilogue.
+  // When Q % 4 == 0 each output row goes through LDS (the patch is free
+  // once every wavefront has finished its MFMAs), so that a lane stores 16
+  // bytes of four consecutive pixels of one channel and a wavefront writes
+  // whole 448-byte row runs, instead of four 4-byte values of four channels.
+  constexpr int kStageRow = kCols + 4;  // one channel's staged row, padded
+  constexpr int kGroups4 = kCols / 4;   // 16-byte groups per channel row
+  constexpr int kItems = kChannels * kGroups4 / kThreads;
+  static_assert(kChannels * kStageRow <= kPatchMax && kItems * kThreads == kChannels * kGroups4, "stage");
+  if ((q & 3) == 0) {
+    float* stage = patch;
+#pragma unroll
+    for (int rb = 0; rb < kRows; ++rb) {
+      const int oh = oh0 + rb;
+      __syncthreads();  // the patch (first row) or the previous row's stage is no longer read
+#pragma unroll
+      for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stage[(16 * wv + 4 * quarter + e) * kStageRow + b * 16 + lane16] = acc[rb][b][e];
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < kItems; ++it) {
+        const int item = tid + it * kThreads;
+        const int local = item / kGroups4;
+        const int g4 = item - local * kGroups4;
+        const int kk = k0 + local;
+        const int ow = ow0 + 4 * g4;
+        if (oh >= p || kk >= k || ow >= q) continue;  // Q % 4 == 0: a group is whole or outside
+        const size_t at = ((static_cast<size_t>(img) * k + kk) * p + oh) * q + ow;
+        f32x4 v = *reinterpret_cast<const f32x4*>(stage + local * kStageRow + 4 * g4);
+        f32x4 res = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (EPI == kBatchNormAddRelu) res = *reinterpret_cast<const f32x4*>(residual + at);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (EPI != kPlain) v[e] = fmaf(v[e], epi_mul[local], epi_add[local]);
+          if (EPI == kBatchNormAddRelu) v[e] += res[e];
+          if (EPI == kBatchNormRelu || EPI == kBatchNormAddRelu) v[e] = fmaxf(v[e], 0.0f);
+        }
+        *reinterpret_cast<f32x4*>(output + at) = v;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < kRows; ++rb) {
     const int oh = oh0 + rb;
